@@ -1,0 +1,165 @@
+// common.hpp -- shared device and host helpers for the gfx950 kernels.
+//
+// Wave64 reductions use DPP lane permutes inside 16-lane rows and
+// v_readlane across rows, so a row reduction finishes without LDS traffic
+// and every lane of a group ends with the bitwise-identical value.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <tuple>
+#include <utility>
+
+#include "fence/ops.h"
+
+namespace fence {
+
+constexpr int kWave = 64;
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ memory
+
+template <bool NT>
+__device__ __forceinline__ f4 ld4(const float* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+    else return *reinterpret_cast<const f4*>(p);
+}
+
+template <bool NT>
+__device__ __forceinline__ void st4(float* p, f4 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+    else *reinterpret_cast<f4*>(p) = v;
+}
+
+__device__ __forceinline__ float dot4(f4 a) {
+    // pairwise: (a0^2 + a1^2) + (a2^2 + a3^2)
+    return (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
+}
+
+// ------------------------------------------------------------- reductions
+
+struct OpAdd {
+    __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// DPP controls (GFX9 encoding).
+enum : int {
+    kDppQuadXor1 = 0xB1,   // quad_perm [1,0,3,2]
+    kDppQuadXor2 = 0x4E,   // quad_perm [2,3,0,1]
+    kDppHalfMirror = 0x141,// lane i <- lane 7-i within 8
+    kDppMirror = 0x140,    // lane i <- lane 15-i within 16
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// xor-16 exchange inside 32-lane halves (ds_swizzle bit mode: and=0x1F, xor=0x10)
+__device__ __forceinline__ float swz_xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Reduction over aligned groups of G lanes (G in {8,16,32}); every lane of a
+// group receives the group result.  All 64 lanes must be active.
+template <int G, class Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+    static_assert(G == 8 || G == 16 || G == 32, "group size");
+    v = op(v, dpp<kDppQuadXor1>(v));
+    v = op(v, dpp<kDppQuadXor2>(v));
+    v = op(v, dpp<kDppHalfMirror>(v));
+    if constexpr (G >= 16) v = op(v, dpp<kDppMirror>(v));
+    if constexpr (G >= 32) v = op(v, swz_xor16(v));
+    return v;
+}
+
+// Full-wave reduction; the result is wave-uniform.  All 64 lanes must be active.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = group_reduce<16>(v, op);
+    return op(op(readlane(v, 0), readlane(v, 16)), op(readlane(v, 32), readlane(v, 48)));
+}
+
+// Workgroup reduction for blockDim.x = NWAVES * 64.  `scratch` holds NWAVES
+// floats of LDS.  Ends with a barrier-protected read, so the result is
+// uniform across the workgroup; callers may reuse `scratch` only after
+// another __syncthreads().
+template <int NWAVES, class Op>
+__device__ __forceinline__ float block_reduce(float v, Op op, float* scratch) {
+    v = wave_reduce(v, op);
+    if constexpr (NWAVES == 1) {
+        return v;
+    } else {
+        const int wave = threadIdx.x / kWave;
+        if ((threadIdx.x % kWave) == 0) scratch[wave] = v;
+        __syncthreads();
+        float r = scratch[0];
+#pragma unroll
+        for (int i = 1; i < NWAVES; ++i) r = op(r, scratch[i]);
+        return r;
+    }
+}
+
+// Runtime wave count version (blockDim.x multiple of 64, at most 16 waves).
+template <class Op>
+__device__ __forceinline__ float block_reduce_dyn(float v, Op op, float* scratch) {
+    v = wave_reduce(v, op);
+    const int nwaves = blockDim.x / kWave;
+    if (nwaves == 1) return v;
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x % kWave) == 0) scratch[wave] = v;
+    __syncthreads();
+    float r = scratch[0];
+    for (int i = 1; i < nwaves; ++i) r = op(r, scratch[i]);
+    return r;
+}
+
+// ------------------------------------------------------------------- host
+
+inline bool aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+inline int hip_status(hipError_t e) {
+    return e == hipSuccess ? FENCE_SUCCESS : FENCE_ERROR_HIP_BASE + static_cast<int>(e);
+}
+
+template <class... KArgs, class Tuple, size_t... I>
+inline int launch_impl(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
+                       hipStream_t stream, Tuple& args, std::index_sequence<I...>) {
+    void* ptrs[] = {static_cast<void*>(&std::get<I>(args))..., nullptr};
+    return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block,
+                                      ptrs, shmem, stream));
+}
+
+// Launch `kernel` and return the status of this launch (not of earlier calls).
+template <class... KArgs, class... Args>
+inline int launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
+                  hipStream_t stream, Args&&... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+    std::tuple<KArgs...> packed(std::forward<Args>(args)...);
+    return launch_impl(kernel, grid, block, shmem, stream, packed,
+                       std::index_sequence_for<KArgs...>{});
+}
+
+inline unsigned grid_1d(int64_t units, int64_t per_block, int64_t cap = 1 << 30) {
+    int64_t g = (units + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return static_cast<unsigned>(g);
+}
+
+}  // namespace fence

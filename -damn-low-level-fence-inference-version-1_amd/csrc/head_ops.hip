@@ -1,0 +1,410 @@
+// head_ops.hip -- per-head RMSNorm, RoPE (NeoX and interleaved) and their
+// fusions with RMSNorm, on gfx950.
+//
+// Reference math:
+//   per-head norm  rms_norm_per_head, src/kernels/ops.cuh:66-103
+//   RoPE NeoX      apply_rope,        src/kernels/ops.cuh:115-177
+//   RoPE interleaved: pairs (2p, 2p+1) of the comment, src/kernels/ops.cuh:109-113
+//   freq[p] = 1.0f / powf(base, (float)(2p)/(float)hd)    (ops.cuh:133),
+//   a = (float)pos * freq[p];  x0' = x0 cos a - x1 sin a;  x1' = x0 sin a + x1 cos a.
+//
+// Layout of the vector kernel: one workgroup per token.  A token's q and k
+// heads are cut into "units" of 8 floats, elements [4i, 4i+4) and
+// [hd/2 + 4i, hd/2 + 4i + 4) of one head (i < hd/8), so a lane holds four
+// whole NeoX pairs -- or four whole interleaved pairs -- and never needs a
+// partner lane.  A head is hd/8 consecutive lanes, so the per-head sum of
+// squares is a DPP reduction inside a 16-lane row (hd = 128).
+// freq[] is computed on the host (exactly the reference expression) and
+// passed in the kernel arguments; cos/sin of the token's hd/2 angles are
+// computed once per token into LDS and shared by all heads.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace fence {
+
+enum { kRopeNone = -1, kRopeNeox = FENCE_ROPE_NEOX, kRopeInter = FENCE_ROPE_INTERLEAVED };
+enum { kNormNone = 0, kNormRow = 1, kNormHead = 2 };
+
+constexpr int kMaxHalf = 128;  // head_dim <= 256 for RoPE
+
+struct InvFreq {
+    float v[kMaxHalf];
+};
+
+namespace {
+
+constexpr int kMaxSlots = 8;
+
+template <int ROPE, int NORM, int G>
+__global__ __launch_bounds__(256) void head_ops_vec_kernel(
+    float* qo, const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
+    int nkv, int slots, float eps, const int32_t* positions, int pos0, InvFreq tab) {
+    constexpr int HD = 8 * G;
+    constexpr int HALF = 4 * G;
+    __shared__ __align__(16) float cs[2 * HALF];  // cos[HALF] then sin[HALF]
+    __shared__ float red[4];
+    const int T = blockDim.x;
+    const int U = (nq + nkv) * G;
+    const float inv_row_n = 1.0f / static_cast<float>(nq * HD);
+    (void)inv_row_n;
+
+    for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+        const int pos = positions ? positions[t] : pos0 + static_cast<int>(t);
+        const float* qrow_in = qi + t * nq * HD;
+        float* qrow_out = qo + t * nq * HD;
+        float* krow = k + t * nkv * HD;
+
+        f4 a[kMaxSlots], b[kMaxSlots];
+#pragma unroll
+        for (int s = 0; s < kMaxSlots; ++s) {
+            const int u = threadIdx.x + s * T;
+            a[s] = f4(0.0f);
+            b[s] = f4(0.0f);
+            if (s < slots && u < U) {
+                const int h = u / G;
+                const int i = u % G;
+                const float* src = (h < nq) ? qrow_in + h * HD : krow + (h - nq) * HD;
+                a[s] = ld4<false>(src + 4 * i);
+                b[s] = ld4<false>(src + HALF + 4 * i);
+            }
+        }
+
+        if constexpr (ROPE != kRopeNone) {
+            for (int p = threadIdx.x; p < HALF; p += T) {
+                const float ang = static_cast<float>(pos) * tab.v[p];
+                float sn, cn;
+                sincosf(ang, &sn, &cn);
+                cs[p] = cn;
+                cs[HALF + p] = sn;
+            }
+        }
+
+        float rrow = 1.0f;
+        if constexpr (NORM == kNormRow) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int s = 0; s < kMaxSlots; ++s) {
+                const int u = threadIdx.x + s * T;
+                if (s < slots && u < nq * G) ss += dot4(a[s]) + dot4(b[s]);
+            }
+            const float tot = block_reduce_dyn(ss, OpAdd(), red);
+            rrow = rsqrtf(tot / static_cast<float>(nq * HD) + eps);
+        }
+
+        float rh[kMaxSlots];
+        if constexpr (NORM == kNormHead) {
+#pragma unroll
+            for (int s = 0; s < kMaxSlots; ++s) {
+                float ss = 0.0f;
+                if (s < slots) ss = dot4(a[s]) + dot4(b[s]);
+                if (s < slots) {  // slots is uniform: whole waves enter together
+                    const float tot = group_reduce<G>(ss, OpAdd());
+                    rh[s] = rsqrtf(tot / static_cast<float>(HD) + eps);
+                } else {
+                    rh[s] = 1.0f;
+                }
+            }
+        }
+
+        if constexpr (ROPE != kRopeNone || NORM == kNormRow) __syncthreads();
+
+#pragma unroll
+        for (int s = 0; s < kMaxSlots; ++s) {
+            const int u = threadIdx.x + s * T;
+            if (!(s < slots && u < U)) continue;
+            const int h = u / G;
+            const int i = u % G;
+            const bool isq = h < nq;
+            f4 va = a[s];
+            f4 vb = b[s];
+            if constexpr (NORM == kNormRow) {
+                if (isq) {
+                    const float* wr = wq + h * HD;
+                    va = (ld4<false>(wr + 4 * i) * va) * rrow;
+                    vb = (ld4<false>(wr + HALF + 4 * i) * vb) * rrow;
+                }
+            } else if constexpr (NORM == kNormHead) {
+                const float* wr = isq ? wq : wk;
+                va = (ld4<false>(wr + 4 * i) * va) * rh[s];
+                vb = (ld4<false>(wr + HALF + 4 * i) * vb) * rh[s];
+            }
+            if constexpr (ROPE == kRopeNeox) {
+                const f4 c = *reinterpret_cast<const f4*>(cs + 4 * i);
+                const f4 sn = *reinterpret_cast<const f4*>(cs + HALF + 4 * i);
+                const f4 x0 = va, x1 = vb;
+                va = x0 * c - x1 * sn;
+                vb = x0 * sn + x1 * c;
+            } else if constexpr (ROPE == kRopeInter) {
+                const f2 ca = *reinterpret_cast<const f2*>(cs + 2 * i);
+                const f2 sa = *reinterpret_cast<const f2*>(cs + HALF + 2 * i);
+                const f2 cb = *reinterpret_cast<const f2*>(cs + HALF / 2 + 2 * i);
+                const f2 sb = *reinterpret_cast<const f2*>(cs + HALF + HALF / 2 + 2 * i);
+                const f4 x = va, y = vb;
+                va.x = x.x * ca.x - x.y * sa.x;
+                va.y = x.x * sa.x + x.y * ca.x;
+                va.z = x.z * ca.y - x.w * sa.y;
+                va.w = x.z * sa.y + x.w * ca.y;
+                vb.x = y.x * cb.x - y.y * sb.x;
+                vb.y = y.x * sb.x + y.y * cb.x;
+                vb.z = y.z * cb.y - y.w * sb.y;
+                vb.w = y.z * sb.y + y.w * cb.y;
+            }
+            float* dst = isq ? qrow_out + h * HD : krow + (h - nq) * HD;
+            st4<false>(dst + 4 * i, va);
+            st4<false>(dst + HALF + 4 * i, vb);
+        }
+        __syncthreads();  // cs[] and red[] are rewritten for the next token
+    }
+}
+
+// Any head_dim and alignment.  One workgroup per token, one wave per head.
+template <int ROPE, int NORM>
+__global__ __launch_bounds__(256) void head_ops_scalar_kernel(
+    float* qo, const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
+    int nkv, int hd, float eps, const int32_t* positions, int pos0, InvFreq tab) {
+    __shared__ float red[4];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int half = hd / 2;
+    for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+        const int pos = positions ? positions[t] : pos0 + static_cast<int>(t);
+        const float* qrow_in = qi + t * nq * hd;
+        float* qrow_out = qo + t * nq * hd;
+        float* krow = k + t * nkv * hd;
+
+        float rrow = 1.0f;
+        if constexpr (NORM == kNormRow) {
+            float ss = 0.0f;
+            for (int e = threadIdx.x; e < nq * hd; e += 256) ss += qrow_in[e] * qrow_in[e];
+            const float tot = block_reduce<4>(ss, OpAdd(), red);
+            rrow = rsqrtf(tot / static_cast<float>(nq * hd) + eps);
+        }
+
+        for (int h = wave; h < nq + nkv; h += 4) {
+            const bool isq = h < nq;
+            const float* src = isq ? qrow_in + h * hd : krow + (h - nq) * hd;
+            float* dst = isq ? qrow_out + h * hd : krow + (h - nq) * hd;
+            const float* wr = nullptr;
+            float r = 1.0f;
+            if constexpr (NORM == kNormRow) {
+                if (isq) {
+                    wr = wq + h * hd;
+                    r = rrow;
+                }
+            } else if constexpr (NORM == kNormHead) {
+                wr = isq ? wq : wk;
+                float ss = 0.0f;
+                for (int e = lane; e < hd; e += kWave) ss += src[e] * src[e];
+                r = rsqrtf(wave_reduce(ss, OpAdd()) / static_cast<float>(hd) + eps);
+            }
+            if constexpr (ROPE == kRopeNone) {
+                for (int e = lane; e < hd; e += kWave) dst[e] = wr ? (wr[e] * src[e]) * r : src[e];
+            } else {
+                for (int p = lane; p < half; p += kWave) {
+                    const int i0 = (ROPE == kRopeNeox) ? p : 2 * p;
+                    const int i1 = (ROPE == kRopeNeox) ? p + half : 2 * p + 1;
+                    float x0 = src[i0];
+                    float x1 = src[i1];
+                    if (wr) {
+                        x0 = (wr[i0] * x0) * r;
+                        x1 = (wr[i1] * x1) * r;
+                    }
+                    float sn, cn;
+                    sincosf(static_cast<float>(pos) * tab.v[p], &sn, &cn);
+                    dst[i0] = x0 * cn - x1 * sn;
+                    dst[i1] = x0 * sn + x1 * cn;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int ROPE, int NORM>
+int dispatch_vec(int G, unsigned grid, unsigned threads, hipStream_t s, float* qo, const float* qi,
+                 float* k, const float* wq, const float* wk, int64_t tokens, int nq, int nkv,
+                 int slots, float eps, const int32_t* positions, int pos0, const InvFreq& tab) {
+    switch (G) {
+        case 8:
+            return launch(head_ops_vec_kernel<ROPE, NORM, 8>, dim3(grid), dim3(threads), 0, s, qo, qi,
+                          k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+        case 16:
+            return launch(head_ops_vec_kernel<ROPE, NORM, 16>, dim3(grid), dim3(threads), 0, s, qo,
+                          qi, k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+        case 32:
+            return launch(head_ops_vec_kernel<ROPE, NORM, 32>, dim3(grid), dim3(threads), 0, s, qo,
+                          qi, k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+        default:
+            return FENCE_ERROR_INVALID_VALUE;
+    }
+}
+
+template <int ROPE, int NORM>
+int dispatch(bool vec, int G, unsigned grid, unsigned threads, hipStream_t s, float* qo,
+             const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
+             int nkv, int hd, int slots, float eps, const int32_t* positions, int pos0,
+             const InvFreq& tab) {
+    if (vec)
+        return dispatch_vec<ROPE, NORM>(G, grid, threads, s, qo, qi, k, wq, wk, tokens, nq, nkv,
+                                        slots, eps, positions, pos0, tab);
+    return launch(head_ops_scalar_kernel<ROPE, NORM>, dim3(grid), dim3(256), 0, s, qo, qi, k, wq,
+                  wk, tokens, nq, nkv, hd, eps, positions, pos0, tab);
+}
+
+template <int ROPE>
+int dispatch_norm(int norm, bool vec, int G, unsigned grid, unsigned threads, hipStream_t s,
+                  float* qo, const float* qi, float* k, const float* wq, const float* wk,
+                  int64_t tokens, int nq, int nkv, int hd, int slots, float eps,
+                  const int32_t* positions, int pos0, const InvFreq& tab) {
+    switch (norm) {
+        case kNormNone:
+            return dispatch<ROPE, kNormNone>(vec, G, grid, threads, s, qo, qi, k, wq, wk, tokens,
+                                             nq, nkv, hd, slots, eps, positions, pos0, tab);
+        case kNormRow:
+            return dispatch<ROPE, kNormRow>(vec, G, grid, threads, s, qo, qi, k, wq, wk, tokens, nq,
+                                            nkv, hd, slots, eps, positions, pos0, tab);
+        case kNormHead:
+            return dispatch<ROPE, kNormHead>(vec, G, grid, threads, s, qo, qi, k, wq, wk, tokens,
+                                             nq, nkv, hd, slots, eps, positions, pos0, tab);
+        default:
+            return FENCE_ERROR_INVALID_VALUE;
+    }
+}
+
+bool ok4(const void* p) { return p == nullptr || aligned(p, 4); }
+bool ok16(const void* p) { return p == nullptr || aligned(p, 16); }
+
+}  // namespace
+
+// Host computation of the reference's per-pair frequency (ops.cuh:133).
+// A one-entry cache per host thread avoids recomputing hd/2 powf calls for
+// every decode step with the same (base, head_dim).
+void rope_inv_freq_host(float* out, int hd, float base) {
+    thread_local int c_hd = -1;
+    thread_local uint32_t c_base_bits = 0;
+    thread_local float c_vals[kMaxHalf];
+    const uint32_t bits = __builtin_bit_cast(uint32_t, base);
+    if (c_hd != hd || c_base_bits != bits) {
+        for (int p = 0; p < hd / 2; ++p)
+            c_vals[p] = 1.0f / powf(base, static_cast<float>(2 * p) / static_cast<float>(hd));
+        c_hd = hd;
+        c_base_bits = bits;
+    }
+    for (int p = 0; p < hd / 2; ++p) out[p] = c_vals[p];
+}
+
+// Shared entry for every head-structured op.
+//   qo/qi: q output/input [tokens][nq][hd] (equal for the in-place forms)
+//   k:     [tokens][nkv][hd], in place
+//   norm:  none | row (q row, weight wq[nq*hd]) | head (wq[hd], wk[hd])
+int head_ops_launch(float* qo, const float* qi, float* k, const float* wq, const float* wk,
+                    int64_t tokens, int nq, int nkv, int hd, float eps, const int32_t* positions,
+                    int pos0, float base, int rope, int norm, hipStream_t s) {
+    if (tokens < 0 || nq < 0 || nkv < 0 || hd <= 0) return FENCE_ERROR_INVALID_VALUE;
+    if (rope != kRopeNone && rope != kRopeNeox && rope != kRopeInter) return FENCE_ERROR_INVALID_VALUE;
+    if (nq > 0 && (!qo || !qi)) return FENCE_ERROR_INVALID_VALUE;
+    if (nkv > 0 && !k) return FENCE_ERROR_INVALID_VALUE;
+    if (norm == kNormRow && nq > 0 && !wq) return FENCE_ERROR_INVALID_VALUE;
+    if (norm == kNormHead && ((nq > 0 && !wq) || (nkv > 0 && !wk))) return FENCE_ERROR_INVALID_VALUE;
+    if (rope != kRopeNone) {
+        if (hd % 2 != 0 || hd > 2 * kMaxHalf) return FENCE_ERROR_INVALID_VALUE;
+        if (!(base > 0.0f) || !std::isfinite(base)) return FENCE_ERROR_INVALID_VALUE;
+    }
+    if (!ok4(qo) || !ok4(qi) || !ok4(k) || !ok4(wq) || !ok4(wk) || !ok4(positions))
+        return FENCE_ERROR_INVALID_VALUE;
+    if (tokens == 0 || nq + nkv == 0) return FENCE_SUCCESS;
+    if (nq == 0) {  // keep q pointers valid for address arithmetic only
+        qo = k;
+        qi = k;
+    }
+    if (nkv == 0) k = qo;
+
+    InvFreq tab{};
+    if (rope != kRopeNone) rope_inv_freq_host(tab.v, hd, base);
+
+    const int G = hd / 8;
+    bool vec = (hd == 64 || hd == 128 || hd == 256) && ok16(qo) && ok16(qi) && ok16(k) &&
+               ok16(wq) && ok16(wk);
+    unsigned threads = 256;
+    int slots = 0;
+    if (vec) {
+        const int64_t U = static_cast<int64_t>(nq + nkv) * G;
+        // smallest idle-lane count over workgroup sizes 64..256, preferring larger groups
+        int64_t best_idle = -1;
+        for (int th = 256; th >= 64; th -= 64) {
+            const int64_t sl = (U + th - 1) / th;
+            if (sl > kMaxSlots) continue;
+            const int64_t idle = sl * th - U;
+            if (best_idle < 0 || idle < best_idle) {
+                best_idle = idle;
+                threads = th;
+                slots = static_cast<int>(sl);
+            }
+        }
+        if (best_idle < 0) vec = false;
+    }
+    const unsigned grid = grid_1d(tokens, 1, 1 << 20);
+    switch (rope) {
+        case kRopeNone:
+            return dispatch_norm<kRopeNone>(norm, vec, G, grid, threads, s, qo, qi, k, wq, wk,
+                                            tokens, nq, nkv, hd, slots, eps, positions, pos0, tab);
+        case kRopeNeox:
+            return dispatch_norm<kRopeNeox>(norm, vec, G, grid, threads, s, qo, qi, k, wq, wk,
+                                            tokens, nq, nkv, hd, slots, eps, positions, pos0, tab);
+        default:
+            return dispatch_norm<kRopeInter>(norm, vec, G, grid, threads, s, qo, qi, k, wq, wk,
+                                             tokens, nq, nkv, hd, slots, eps, positions, pos0, tab);
+    }
+}
+
+}  // namespace fence
+
+using fence::head_ops_launch;
+
+extern "C" int fence_rms_norm_per_head(float* x, const float* w, int n_heads, int head_dim,
+                                       float eps, hipStream_t stream) {
+    if (!w) return FENCE_ERROR_INVALID_VALUE;
+    return head_ops_launch(x, x, nullptr, w, nullptr, 1, n_heads, 0, head_dim, eps, nullptr, 0,
+                           1.0f, fence::kRopeNone, fence::kNormHead, stream);
+}
+
+extern "C" int fence_apply_rope(float* q, float* k, int head_dim, int n_q_heads, int n_kv_heads,
+                                int pos, float freq_base, hipStream_t stream) {
+    return head_ops_launch(q, q, k, nullptr, nullptr, 1, n_q_heads, n_kv_heads, head_dim, 0.0f,
+                           nullptr, pos, freq_base, fence::kRopeNeox, fence::kNormNone, stream);
+}
+
+extern "C" int fence_rope(float* q, float* k, int64_t tokens, int n_q_heads, int n_kv_heads,
+                          int head_dim, const int32_t* positions, int pos0, float freq_base,
+                          int style, hipStream_t stream) {
+    if (style != FENCE_ROPE_NEOX && style != FENCE_ROPE_INTERLEAVED) return FENCE_ERROR_INVALID_VALUE;
+    return head_ops_launch(q, q, k, nullptr, nullptr, tokens, n_q_heads, n_kv_heads, head_dim, 0.0f,
+                           positions, pos0, freq_base, style, fence::kNormNone, stream);
+}
+
+extern "C" int fence_qk_norm_rope(float* q, float* k, const float* q_norm_w, const float* k_norm_w,
+                                  int64_t tokens, int n_q_heads, int n_kv_heads, int head_dim,
+                                  float eps, const int32_t* positions, int pos0, float freq_base,
+                                  int style, hipStream_t stream) {
+    if (style != FENCE_ROPE_NEOX && style != FENCE_ROPE_INTERLEAVED) return FENCE_ERROR_INVALID_VALUE;
+    return head_ops_launch(q, q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads, head_dim,
+                           eps, positions, pos0, freq_base, style, fence::kNormHead, stream);
+}
+
+extern "C" int fence_rms_norm_rope(float* out, const float* x, const float* w, float* k,
+                                   int64_t tokens, int n_q_heads, int n_kv_heads, int head_dim,
+                                   float eps, const int32_t* positions, int pos0, float freq_base,
+                                   int style, hipStream_t stream) {
+    if (style != FENCE_ROPE_NEOX && style != FENCE_ROPE_INTERLEAVED) return FENCE_ERROR_INVALID_VALUE;
+    if (n_q_heads <= 0 || !w) return FENCE_ERROR_INVALID_VALUE;
+    return head_ops_launch(out, x, k, w, nullptr, tokens, n_q_heads, n_kv_heads, head_dim, eps,
+                           positions, pos0, freq_base, style, fence::kNormRow, stream);
+}
+
+extern "C" int fence_rope_inv_freq(float* inv_freq, int head_dim, float freq_base) {
+    if (!inv_freq || head_dim <= 0 || head_dim % 2 != 0 || head_dim > 2 * fence::kMaxHalf)
+        return FENCE_ERROR_INVALID_VALUE;
+    fence::rope_inv_freq_host(inv_freq, head_dim, freq_base);
+    return FENCE_SUCCESS;
+}

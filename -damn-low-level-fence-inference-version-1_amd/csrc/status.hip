@@ -1,0 +1,12 @@
+// status.hip -- status strings and version of the C ABI (host only).
+#include "common.hpp"
+
+extern "C" const char* fence_status_string(int status) {
+    if (status == FENCE_SUCCESS) return "success";
+    if (status == FENCE_ERROR_INVALID_VALUE) return "invalid value (shape, null or misaligned pointer)";
+    if (status > FENCE_ERROR_HIP_BASE)
+        return hipGetErrorString(static_cast<hipError_t>(status - FENCE_ERROR_HIP_BASE));
+    return "unknown status";
+}
+
+extern "C" const char* fence_version(void) { return "fence-mi355x 0.1.0 (gfx950)"; }

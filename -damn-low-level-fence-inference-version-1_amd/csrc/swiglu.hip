@@ -1,0 +1,96 @@
+// swiglu.hip -- out = silu(gate) * up on gfx950.
+//
+// Follows silu_elementwise_mul, src/kernels/ops.cuh:183-202:
+//   out[i] = (g / (1.0f + expf(-g))) * up[i],  g = gate[i].
+// Streaming kernel: every workgroup owns UNROLL*256 consecutive float4s and
+// issues all of its 128-bit loads before any math, so each wave keeps
+// 2*UNROLL loads in flight; outputs go out with non-temporal stores.
+// out may alias gate or up: each element is read and written by the same
+// lane, reads first.
+#include "common.hpp"
+
+namespace fence {
+namespace {
+
+constexpr int kSwigluThreads = 256;
+constexpr int kSwigluUnroll = 4;
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return (g / (1.0f + expf(-g))) * u;
+}
+
+template <int UNROLL>
+__global__ __launch_bounds__(kSwigluThreads) void swiglu_vec_kernel(
+    float* out, const float* gate, const float* up, int64_t n4) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (kSwigluThreads * UNROLL) + threadIdx.x;
+    f4 g[UNROLL], u[UNROLL];
+#pragma unroll
+    for (int j = 0; j < UNROLL; ++j) {
+        const int64_t i = base + static_cast<int64_t>(j) * kSwigluThreads;
+        if (i < n4) {
+            g[j] = ld4<true>(gate + 4 * i);
+            u[j] = ld4<true>(up + 4 * i);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < UNROLL; ++j) {
+        const int64_t i = base + static_cast<int64_t>(j) * kSwigluThreads;
+        if (i < n4) {
+            f4 r;
+            r.x = silu_mul(g[j].x, u[j].x);
+            r.y = silu_mul(g[j].y, u[j].y);
+            r.z = silu_mul(g[j].z, u[j].z);
+            r.w = silu_mul(g[j].w, u[j].w);
+            st4<true>(out + 4 * i, r);
+        }
+    }
+}
+
+// Scalar form for unaligned pointers and the n % 4 tail.
+__global__ __launch_bounds__(kSwigluThreads) void swiglu_scalar_kernel(
+    float* out, const float* gate, const float* up, int64_t begin, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kSwigluThreads;
+    for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kSwigluThreads + threadIdx.x; i < n;
+         i += stride)
+        out[i] = silu_mul(gate[i], up[i]);
+}
+
+int swiglu_launch(float* out, const float* gate, const float* up, int64_t n, hipStream_t s) {
+    if (!out || !gate || !up || n < 0) return FENCE_ERROR_INVALID_VALUE;
+    if (!aligned(out, 4) || !aligned(gate, 4) || !aligned(up, 4)) return FENCE_ERROR_INVALID_VALUE;
+    if (n == 0) return FENCE_SUCCESS;
+    const bool vec = aligned(out, 16) && aligned(gate, 16) && aligned(up, 16);
+    int64_t done = 0;
+    if (vec) {
+        const int64_t n4 = n / 4;
+        if (n4 > 0) {
+            const unsigned grid = grid_1d(n4, kSwigluThreads * kSwigluUnroll, int64_t(1) << 31);
+            if (static_cast<int64_t>(grid) * kSwigluThreads * kSwigluUnroll < n4)
+                return FENCE_ERROR_INVALID_VALUE;  // beyond 2^31 workgroups
+            const int st = launch(swiglu_vec_kernel<kSwigluUnroll>, dim3(grid), dim3(kSwigluThreads),
+                                  0, s, out, gate, up, n4);
+            if (st) return st;
+        }
+        done = n4 * 4;
+    }
+    if (done < n) {
+        const unsigned grid = grid_1d(n - done, kSwigluThreads, 65536);
+        return launch(swiglu_scalar_kernel, dim3(grid), dim3(kSwigluThreads), 0, s, out, gate, up,
+                      done, n);
+    }
+    return FENCE_SUCCESS;
+}
+
+}  // namespace
+}  // namespace fence
+
+extern "C" int fence_swiglu(float* out, const float* gate, const float* up, int64_t n,
+                            hipStream_t stream) {
+    return fence::swiglu_launch(out, gate, up, n, stream);
+}
+
+extern "C" int fence_silu_elementwise_mul(float* out, const float* gate, const float* up, int n,
+                                          hipStream_t stream) {
+    if (n < 0) return FENCE_ERROR_INVALID_VALUE;
+    return fence::swiglu_launch(out, gate, up, n, stream);
+}

@@ -1,0 +1,172 @@
+"""ctypes binding of libfence_ops.so, the C ABI declared in include/fence/ops.h.
+
+Used by the tests and by bench.py to call the gfx950 kernels with device
+pointers (for example ``torch.Tensor.data_ptr()``) and a HIP stream handle.
+There is no fallback: if the shared library is missing, loading raises.
+
+Every wrapper raises FenceError on a non-zero status; the raw ctypes
+functions stay reachable through ``lib()`` for status-code tests.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfence_ops.so")
+
+SUCCESS = 0
+EINVAL = 22
+HIP_BASE = 1000
+ROPE_NEOX = 0
+ROPE_INTERLEAVED = 1
+QK8_0 = 32
+Q8_0_BLOCK_BYTES = 34
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> argument types, in the order of include/fence/ops.h
+SIGNATURES = {
+    "fence_rms_norm": (_P, _P, _P, _I, _F, _P),
+    "fence_rms_norm_inplace": (_P, _P, _I, _F, _P),
+    "fence_rms_norm_per_head": (_P, _P, _I, _I, _F, _P),
+    "fence_apply_rope": (_P, _P, _I, _I, _I, _I, _F, _P),
+    "fence_silu_elementwise_mul": (_P, _P, _P, _I, _P),
+    "fence_softmax": (_P, _I, _P),
+    "fence_embed_q8_0": (_P, _P, _I, _I, _P),
+    "fence_rms_norm_rows": (_P, _P, _P, _L, _I, _F, _P),
+    "fence_rope": (_P, _P, _L, _I, _I, _I, _P, _I, _F, _I, _P),
+    "fence_qk_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
+    "fence_rms_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
+    "fence_swiglu": (_P, _P, _P, _L, _P),
+    "fence_softmax_rows": (_P, _L, _I, _L, _P),
+    "fence_softmax_causal": (_P, _L, _I, _I, _P),
+    "fence_embed_q8_0_gather": (_P, _P, _L, _P, _L, _I, _P),
+    "fence_embed_q8_0_gather_rms_norm": (_P, _P, _L, _P, _L, _I, _P, _F, _P),
+    "fence_rope_inv_freq": (_P, _I, _F),
+    "fence_status_string": (_I,),
+    "fence_version": (),
+}
+_RESTYPES = {"fence_status_string": ctypes.c_char_p, "fence_version": ctypes.c_char_p}
+
+_lib = None
+
+
+class FenceError(RuntimeError):
+    def __init__(self, name: str, status: int):
+        self.status = status
+        super().__init__(f"{name} failed with status {status}: {status_string(status)}")
+
+
+def lib(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libfence_ops.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+        handle = ctypes.CDLL(path)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = list(argtypes)
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = handle
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().fence_status_string(status).decode()
+
+
+def version() -> str:
+    return lib().fence_version().decode()
+
+
+def _call(name: str, *args) -> None:
+    st = getattr(lib(), name)(*args)
+    if st != SUCCESS:
+        raise FenceError(name, st)
+
+
+# ----------------------------------------------------------------- wrappers
+# Pointer arguments are integers (device addresses) or None; `stream` is a
+# hipStream_t handle as an integer (0 / None = the null stream).
+
+def rms_norm(out, x, w, n, eps, stream=None):
+    _call("fence_rms_norm", out, x, w, n, eps, stream)
+
+
+def rms_norm_inplace(x, w, n, eps, stream=None):
+    _call("fence_rms_norm_inplace", x, w, n, eps, stream)
+
+
+def rms_norm_per_head(x, w, n_heads, head_dim, eps, stream=None):
+    _call("fence_rms_norm_per_head", x, w, n_heads, head_dim, eps, stream)
+
+
+def apply_rope(q, k, head_dim, n_q_heads, n_kv_heads, pos, freq_base, stream=None):
+    _call("fence_apply_rope", q, k, head_dim, n_q_heads, n_kv_heads, pos, freq_base, stream)
+
+
+def silu_elementwise_mul(out, gate, up, n, stream=None):
+    _call("fence_silu_elementwise_mul", out, gate, up, n, stream)
+
+
+def softmax(x, n, stream=None):
+    _call("fence_softmax", x, n, stream)
+
+
+def embed_q8_0(out, weight, token_id, dim, stream=None):
+    _call("fence_embed_q8_0", out, weight, token_id, dim, stream)
+
+
+def rms_norm_rows(out, x, w, rows, n, eps, stream=None):
+    _call("fence_rms_norm_rows", out, x, w, rows, n, eps, stream)
+
+
+def rope(q, k, tokens, n_q_heads, n_kv_heads, head_dim, positions, pos0, freq_base, style,
+         stream=None):
+    _call("fence_rope", q, k, tokens, n_q_heads, n_kv_heads, head_dim, positions, pos0,
+          freq_base, style, stream)
+
+
+def qk_norm_rope(q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads, head_dim, eps,
+                 positions, pos0, freq_base, style, stream=None):
+    _call("fence_qk_norm_rope", q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads,
+          head_dim, eps, positions, pos0, freq_base, style, stream)
+
+
+def rms_norm_rope(out, x, w, k, tokens, n_q_heads, n_kv_heads, head_dim, eps, positions, pos0,
+                  freq_base, style, stream=None):
+    _call("fence_rms_norm_rope", out, x, w, k, tokens, n_q_heads, n_kv_heads, head_dim, eps,
+          positions, pos0, freq_base, style, stream)
+
+
+def swiglu(out, gate, up, n, stream=None):
+    _call("fence_swiglu", out, gate, up, n, stream)
+
+
+def softmax_rows(x, rows, n, ld, stream=None):
+    _call("fence_softmax_rows", x, rows, n, ld, stream)
+
+
+def softmax_causal(x, heads, sq, sk, stream=None):
+    _call("fence_softmax_causal", x, heads, sq, sk, stream)
+
+
+def embed_q8_0_gather(out, table, vocab, ids, tokens, dim, stream=None):
+    _call("fence_embed_q8_0_gather", out, table, vocab, ids, tokens, dim, stream)
+
+
+def embed_q8_0_gather_rms_norm(out, table, vocab, ids, tokens, dim, w, eps, stream=None):
+    _call("fence_embed_q8_0_gather_rms_norm", out, table, vocab, ids, tokens, dim, w, eps, stream)
+
+
+def rope_inv_freq(head_dim: int, freq_base: float):
+    """Host-side frequencies the RoPE kernels use, as a list of floats."""
+    buf = (ctypes.c_float * (head_dim // 2))()
+    _call("fence_rope_inv_freq", ctypes.cast(buf, ctypes.c_void_p), head_dim, freq_base)
+    return list(buf)

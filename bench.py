@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused per-layer ops on one MI355X.
+
+Workload (Llama-3-8B-shaped prefill, T = 512):
+one step = the three fused ops of that config on seeded synthetic fp32 data
+  gather    fence_embed_q8_0_gather   512 ids from a 128256 x 4096 Q8_0 table
+  norm_rope fence_rms_norm_rope       x [512 x 4096] -> RMSNorm (eps 1e-5) ->
+                                      interleaved RoPE (theta 5e5, pos 0..511);
+                                      K [512 x 8 x 128] RoPE only
+  swiglu    fence_swiglu              gate, up [512 x 14336] -> out
+Throughput = algorithmic bytes (each input read once, each output written
+once) / time, as GB/s, with inputs resident in HBM.  Cold protocol: the step
+rotates over buffer sets totalling more than 1 GiB, so no step finds its data
+in the 256 MB Infinity Cache or the L2s.
+
+Also reported: per-op time and GB/s measured with HIP events on the launch
+stream inside the timed region, the roofline of the dominant kernel (swiglu),
+the Llama-3-8B decode-step op set in microseconds, a device-copy
+calibration, and the CPU baseline (the scalar oracle on one host core,
+timed on a bounded sample of the same step).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "-damn-low-level-fence-inference-version-1_amd")
+sys.path.insert(0, PKG)
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "achieved HBM GB/s and % of peak per fused op; µs per decode-step op set"
+
+# configs[1] shapes
+T = 512
+HIDDEN = 4096
+NQ, NKV, HD = 32, 8, 128
+FFN = 14336
+VOCAB = 128256
+EPS = 1e-5
+THETA = 5e5
+
+Q8_ROW = HIDDEN // 32 * 34
+BYTES = {
+    # write T*HIDDEN fp32 + read T rows of the table + read T int32 ids
+    "gather": T * HIDDEN * 4 + T * Q8_ROW + T * 4,
+    # read x + write out + read w, plus K read + write
+    "norm_rope": 2 * T * NQ * HD * 4 + NQ * HD * 4 + 2 * T * NKV * HD * 4,
+    # read gate + read up + write out
+    "swiglu": 3 * T * FFN * 4,
+}
+STEP_BYTES = sum(BYTES.values())
+DOMINANT = "swiglu"
+KERNEL_NAMES = {"gather": "q8_gather_vec_kernel", "norm_rope": "head_ops_vec_kernel",
+                "swiglu": "swiglu_vec_kernel"}
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warm", action="store_true", help="reuse one buffer set (cache-warm)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--decode-reps", type=int, default=300)
+    return ap.parse_args()
+
+
+def make_q8_0_table(torch, gen, vocab, dim):
+    nb = dim // 32
+    scale = (torch.randn(vocab, nb, device="cuda", generator=gen).abs() * (0.02 / 127.0)).half()
+    qs = torch.randint(-127, 128, (vocab, nb, 32), device="cuda", generator=gen, dtype=torch.int8)
+    table = torch.empty(vocab, nb, 34, dtype=torch.uint8, device="cuda")
+    table[:, :, 0:2] = scale.view(torch.uint8).view(vocab, nb, 2)
+    table[:, :, 2:] = qs.view(torch.uint8)
+    return table
+
+
+class BufferSet:
+    """One step's inputs and outputs."""
+
+    def __init__(self, torch, gen):
+        f = dict(device="cuda", generator=gen)
+        self.ids = torch.randint(0, VOCAB, (T,), dtype=torch.int32, **f)
+        self.emb = torch.empty(T, HIDDEN, device="cuda")
+        self.x = torch.randn(T, HIDDEN, **f)
+        self.q = torch.empty(T, HIDDEN, device="cuda")
+        self.k = torch.randn(T, NKV * HD, **f)
+        self.gate = torch.randn(T, FFN, **f)
+        self.up = torch.randn(T, FFN, **f)
+        self.act = torch.empty(T, FFN, device="cuda")
+
+
+def read_traffic(kernel_key: str):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary, or None if it is not there."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_key}_config1_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    txt = open(path).read()
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(seconds: float):
+    """Scalar oracle on one host core over a bounded sample of the step."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_py import INTERLEAVED, Oracle, make_q8_0_table as np_table
+
+    o = Oracle()
+    rng = np.random.default_rng(1)
+    rows = 64  # sample: 64 of the 512 token rows per op (same per-row shapes)
+    vocab_sample = 4096  # the gather reads random rows; a smaller table keeps setup short
+    table = np_table(rng, vocab_sample, HIDDEN)
+    ids = rng.integers(0, vocab_sample, rows).astype(np.int32)
+    x = rng.standard_normal((rows, HIDDEN)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(HIDDEN)).astype(np.float32)
+    k = rng.standard_normal((rows, NKV, HD)).astype(np.float32)
+    g = rng.standard_normal((rows, FFN)).astype(np.float32)
+    u = rng.standard_normal((rows, FFN)).astype(np.float32)
+    sample_bytes = STEP_BYTES * rows / T
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        o.embed_q8_0_gather(table, vocab_sample, ids, HIDDEN)
+        o.rms_norm_rope(x, w, k, NQ, HD, EPS, None, 0, THETA, INTERLEAVED)
+        o.silu_mul(g, u)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(sample_bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"configs[1] step ops on {rows} of {T} token rows (same per-row shapes), "
+                      f"{reps} reps in {el:.1f} s, oracle incl. numpy wrapper copies"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the ops are independent per token row, so a "
+              "multi-GPU run would shard rows with no communication; run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import fence_ops as F
+
+    torch.cuda.set_device(0)
+    F.lib()
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    table = make_q8_0_table(torch, gen, VOCAB, HIDDEN)
+    w = 1 + 0.1 * torch.randn(HIDDEN, device="cuda", generator=gen)
+    set_bytes = sum(t.numel() * t.element_size() for t in vars(BufferSet(torch, gen)).values())
+    nsets = 1 if args.warm else max(2, -(-(1 << 30) // set_bytes) + 1)
+    sets = [BufferSet(torch, gen) for _ in range(nsets)]
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+
+    def launch(op, b):
+        if op == "gather":
+            F.embed_q8_0_gather(b.emb.data_ptr(), table.data_ptr(), VOCAB, b.ids.data_ptr(), T, HIDDEN, sh)
+        elif op == "norm_rope":
+            F.rms_norm_rope(b.q.data_ptr(), b.x.data_ptr(), w.data_ptr(), b.k.data_ptr(), T, NQ, NKV, HD,
+                            EPS, None, 0, THETA, F.ROPE_INTERLEAVED, sh)
+        else:
+            F.swiglu(b.act.data_ptr(), b.gate.data_ptr(), b.up.data_ptr(), T * FFN, sh)
+
+    ops = list(BYTES)
+    for i in range(args.warmup):
+        for op in ops:
+            launch(op, sets[i % nsets])
+
+    ev = {op: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)] for op in ops}
+    torch.cuda.synchronize()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for i in range(args.steps):
+        b = sets[i % nsets]
+        for op in ops:
+            e0, e1 = ev[op][i]
+            e0.record(stream)
+            launch(op, b)
+            e1.record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_total = t_start.elapsed_time(t_end)
+    ms_per_step = ms_total / args.steps
+
+    per_op = {}
+    for op in ops:
+        ts = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev[op])  # us
+        mean = sum(ts) / len(ts)
+        per_op[op] = {
+            "us_mean": round(mean, 3),
+            "us_p10": round(ts[len(ts) // 10], 3),
+            "us_p50": round(ts[len(ts) // 2], 3),
+            "us_p90": round(ts[(9 * len(ts)) // 10], 3),
+            "bytes": BYTES[op],
+            "GBps": round(BYTES[op] / (mean * 1e-6) / 1e9, 1),
+            "frac_peak": round(BYTES[op] / (mean * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+            "kernel": KERNEL_NAMES[op],
+        }
+
+    value = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
+    dom = per_op[DOMINANT]
+    traffic = read_traffic(DOMINANT)
+    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                "frac": dom["frac_peak"], "traffic": traffic, "kernel": KERNEL_NAMES[DOMINANT],
+                "algorithmic_bytes_per_launch": BYTES[DOMINANT]}
+
+    decode = decode_op_set(torch, F, gen, args.decode_reps)
+    copy_gbps = copy_calibration(torch)
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch generator on device; Q8_0 scales |N(0,0.02)|/127 as fp16, "
+                "int8 uniform [-127,127])",
+        "config": {"workload": "configs[1] Llama-3-8B prefill T=512: q8_0 gather 512x4096 (vocab 128256) "
+                               "+ rms_norm->interleaved RoPE on Q[512x32x128] with RoPE on K[512x8x128] "
+                               "+ swiglu [512x14336]",
+                   "tokens": T, "hidden": HIDDEN, "heads": [NQ, NKV, HD], "ffn": FFN, "vocab": VOCAB,
+                   "cache": "warm" if args.warm else f"cold ({nsets} rotating buffer sets)",
+                   "step_bytes": STEP_BYTES},
+        "frac_peak": round(value / PEAK_HBM_GBPS, 4),
+        "ops": per_op,
+        "roofline": roofline,
+        "decode_op_set_llama3_8b": decode,
+        "copy_calibration_GBps": copy_gbps,
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 4),
+    }
+    print(json.dumps(line), flush=True)
+
+
+def decode_op_set(torch, F, gen, reps):
+    """Llama-3-8B decode-step op set through the single-row entry points:
+    embed -> rms_norm -> interleaved RoPE (32+8 heads) -> softmax over
+    32 x (pos+1) scores (stride max_ctx) -> rms_norm -> swiglu (14336)."""
+    if reps <= 0:
+        return None
+    max_ctx = 4096
+    pos = int(torch.randint(0, max_ctx, (1,), generator=torch.Generator().manual_seed(5)).item())
+    table = make_q8_0_table(torch, gen, VOCAB, HIDDEN)
+    hidden = torch.empty(HIDDEN, device="cuda")
+    normed = torch.empty(HIDDEN, device="cuda")
+    w1 = 1 + 0.1 * torch.randn(HIDDEN, device="cuda", generator=gen)
+    w2 = 1 + 0.1 * torch.randn(HIDDEN, device="cuda", generator=gen)
+    q = torch.randn(NQ * HD, device="cuda", generator=gen)
+    k = torch.randn(NKV * HD, device="cuda", generator=gen)
+    scores = torch.randn(NQ, max_ctx, device="cuda", generator=gen) * (3 / 128 ** 0.5)
+    gate = torch.randn(FFN, device="cuda", generator=gen)
+    up = torch.randn(FFN, device="cuda", generator=gen)
+    s = torch.cuda.current_stream()
+    sh = s.cuda_stream
+    tok = 9707
+
+    def step():
+        F.embed_q8_0(hidden.data_ptr(), table.data_ptr(), tok, HIDDEN, sh)
+        F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w1.data_ptr(), HIDDEN, 1e-5, sh)
+        F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, THETA, F.ROPE_INTERLEAVED, sh)
+        F.softmax_rows(scores.data_ptr(), NQ, pos + 1, max_ctx, sh)
+        F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), HIDDEN, 1e-5, sh)
+        F.silu_elementwise_mul(gate.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh)
+
+    for _ in range(20):
+        step()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        step()
+        e1.record(s)
+        ts.append((e0, e1))
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) * 1e3 for a, b in ts)
+    out = {"us_p50": round(us[len(us) // 2], 2), "us_p10": round(us[len(us) // 10], 2),
+           "us_p90": round(us[(9 * len(us)) // 10], 2), "pos": pos, "launches": 6, "target_us": 60}
+
+    # the same sequence captured once in a HIP graph and replayed
+    try:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(s)
+        with torch.cuda.stream(side):
+            step()  # warm on the capture stream
+        s.wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            sh_cap = torch.cuda.current_stream().cuda_stream
+            F.embed_q8_0(hidden.data_ptr(), table.data_ptr(), tok, HIDDEN, sh_cap)
+            F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w1.data_ptr(), HIDDEN, 1e-5, sh_cap)
+            F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, THETA, F.ROPE_INTERLEAVED, sh_cap)
+            F.softmax_rows(scores.data_ptr(), NQ, pos + 1, max_ctx, sh_cap)
+            F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), HIDDEN, 1e-5, sh_cap)
+            F.silu_elementwise_mul(gate.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh_cap)
+        for _ in range(10):
+            g.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+            ts.append((e0, e1))
+        torch.cuda.synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 for a, b in ts)
+        out["graph_us_p50"] = round(us[len(us) // 2], 2)
+    except Exception as exc:  # graph capture is optional for the report
+        out["graph_error"] = str(exc)[:200]
+    return out
+
+
+def copy_calibration(torch):
+    """Device-to-device copy of 1 GiB: the practical streaming ceiling."""
+    n = (1 << 30) // 4
+    src = torch.empty(n, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    return round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)
+
+
+if __name__ == "__main__":
+    main()

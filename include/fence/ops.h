@@ -1,0 +1,185 @@
+/*
+ * fence/ops.h -- C ABI of the MI355X (gfx950) fused per-layer ops.
+ *
+ * This is the drop-in boundary for the reference's header-only CUDA launchers
+ * (src/kernels/ops.cuh, src/kernels/gemv_q8_0.cuh of
+ * eeea2222/-Damn-Low-Level-Fence-Inference-version-1).  Every entry point
+ * takes caller-owned device pointers and a HIP stream, launches
+ * asynchronously on that stream and returns an int status.
+ *
+ * Conventions (all entry points):
+ *   - returns FENCE_SUCCESS (0), FENCE_ERROR_INVALID_VALUE (22 = EINVAL) for a
+ *     bad shape, a null pointer or a pointer that is not 4-byte aligned
+ *     (checked on the host before anything is launched), or
+ *     FENCE_ERROR_HIP_BASE + hipError_t when the launch itself fails;
+ *   - never allocates, never synchronises, never exits; no global mutable
+ *     state, so calls are re-entrant from any host thread;
+ *   - 16-byte aligned rows take the 128-bit vector kernels; other alignments
+ *     take scalar kernels with the same results (not an error);
+ *   - in-place forms the reference's callers rely on keep working:
+ *     rms_norm(out == x) and silu_elementwise_mul(out == gate or out == up).
+ *   - fp32 results agree with the reference formulas to 1e-5 of the row's
+ *     largest magnitude; Q8_0 dequantisation is bit-exact.
+ *
+ * Including this header from a non-HIP compiler needs -D__HIP_PLATFORM_AMD__
+ * (the usual requirement of hip_runtime_api.h).
+ */
+#ifndef FENCE_OPS_H
+#define FENCE_OPS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    FENCE_SUCCESS = 0,
+    FENCE_ERROR_INVALID_VALUE = 22,
+    FENCE_ERROR_HIP_BASE = 1000
+};
+
+/* RoPE pairing.  NEOX pairs (p, p + head_dim/2), as the reference's code
+ * (src/kernels/ops.cuh:138-139); INTERLEAVED pairs (2p, 2p+1), as the
+ * comment above it (src/kernels/ops.cuh:109-113). */
+enum {
+    FENCE_ROPE_NEOX = 0,
+    FENCE_ROPE_INTERLEAVED = 1
+};
+
+/* Q8_0 block: fp16 scale then 32 int8 values, 34 bytes, no padding
+ * (src/kernels/q8_0_types.h:8-17). */
+#define FENCE_QK8_0 32
+#define FENCE_Q8_0_BLOCK_BYTES 34
+
+/* ---------------------------------------------------------------------------
+ * One-to-one replacements of the reference launchers (same argument order and
+ * meaning; the stream argument is required in the C ABI).
+ * ------------------------------------------------------------------------ */
+
+/* Replaces rms_norm, src/kernels/ops.cuh:47-51.
+ * out[i] = w[i] * x[i] * rsqrt(mean(x^2) + eps); out may equal x. */
+int fence_rms_norm(float* out, const float* x, const float* w, int n,
+                   float eps, hipStream_t stream);
+
+/* Replaces rms_norm_inplace, src/kernels/ops.cuh:54-60. */
+int fence_rms_norm_inplace(float* x, const float* w, int n, float eps,
+                           hipStream_t stream);
+
+/* Replaces rms_norm_per_head, src/kernels/ops.cuh:97-103.
+ * x [n_heads][head_dim] normalised per head in place with w[head_dim]. */
+int fence_rms_norm_per_head(float* x, const float* w, int n_heads,
+                            int head_dim, float eps, hipStream_t stream);
+
+/* Replaces apply_rope, src/kernels/ops.cuh:169-177 (NeoX pairing, one
+ * position for all heads).  q [n_q_heads][head_dim], k [n_kv_heads][head_dim]
+ * rotated in place; head_dim even and <= 256. */
+int fence_apply_rope(float* q, float* k, int head_dim, int n_q_heads,
+                     int n_kv_heads, int pos, float freq_base,
+                     hipStream_t stream);
+
+/* Replaces silu_elementwise_mul, src/kernels/ops.cuh:197-202.
+ * out[i] = gate[i] / (1 + exp(-gate[i])) * up[i]; out may equal gate or up. */
+int fence_silu_elementwise_mul(float* out, const float* gate, const float* up,
+                               int n, hipStream_t stream);
+
+/* Replaces softmax, src/kernels/ops.cuh:248-251 (in place, one vector). */
+int fence_softmax(float* x, int n, hipStream_t stream);
+
+/* Replaces embed_q8_0, src/kernels/gemv_q8_0.cuh:31-36.
+ * out[dim] = dequantised row token_id of the Q8_0 table `weight`
+ * ([vocab][dim/32] blocks).  dim % 32 == 0.  Like the reference this form
+ * has no vocab argument and cannot check token_id < vocab; use
+ * fence_embed_q8_0_gather for checked lookups. */
+int fence_embed_q8_0(float* out, const void* weight, int token_id, int dim,
+                     hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Batched and fused forms.  These compose the reference's single-row ops over
+ * many tokens (its prefill is a per-token loop, src/model/qwen3.cu:478-481)
+ * and fuse neighbouring ops so intermediates stay in registers.
+ *
+ * Token positions: positions[t] if `positions` (device, int32[tokens]) is not
+ * NULL, else pos0 + t.
+ * ------------------------------------------------------------------------ */
+
+/* rms_norm on each of `rows` rows of length n (src/kernels/ops.cuh:17-51
+ * per row).  out may equal x. */
+int fence_rms_norm_rows(float* out, const float* x, const float* w,
+                        int64_t rows, int n, float eps, hipStream_t stream);
+
+/* RoPE over tokens: q [tokens][n_q_heads][head_dim],
+ * k [tokens][n_kv_heads][head_dim] (k may be NULL when n_kv_heads == 0),
+ * style FENCE_ROPE_NEOX or FENCE_ROPE_INTERLEAVED (apply_rope,
+ * src/kernels/ops.cuh:115-177, per token). */
+int fence_rope(float* q, float* k, int64_t tokens, int n_q_heads,
+               int n_kv_heads, int head_dim, const int32_t* positions,
+               int pos0, float freq_base, int style, hipStream_t stream);
+
+/* Per-head RMSNorm of q (weight q_norm_w[head_dim]) and k (k_norm_w) fused
+ * with RoPE, per token: the sequence rms_norm_per_head(q), rms_norm_per_head(k),
+ * apply_rope of src/model/qwen3.cu:293-299 in one pass over q and k. */
+int fence_qk_norm_rope(float* q, float* k, const float* q_norm_w,
+                       const float* k_norm_w, int64_t tokens, int n_q_heads,
+                       int n_kv_heads, int head_dim, float eps,
+                       const int32_t* positions, int pos0, float freq_base,
+                       int style, hipStream_t stream);
+
+/* out_t = RoPE(rms_norm(x_t, w)) for x [tokens][n_q_heads*head_dim],
+ * w [n_q_heads*head_dim], the normalised row viewed as n_q_heads heads; k
+ * (may be NULL) gets RoPE only.  out may equal x. */
+int fence_rms_norm_rope(float* out, const float* x, const float* w, float* k,
+                        int64_t tokens, int n_q_heads, int n_kv_heads,
+                        int head_dim, float eps, const int32_t* positions,
+                        int pos0, float freq_base, int style,
+                        hipStream_t stream);
+
+/* silu_elementwise_mul with a 64-bit element count. */
+int fence_swiglu(float* out, const float* gate, const float* up, int64_t n,
+                 hipStream_t stream);
+
+/* softmax on `rows` rows of n values, row stride ld >= n (the decode
+ * attention softmax over seq_len scores per head, src/kernels/ops.cuh:357-391,
+ * scores stride max_ctx).  In place. */
+int fence_softmax_rows(float* x, int64_t rows, int n, int64_t ld,
+                       hipStream_t stream);
+
+/* Causal softmax over x [heads][sq][sk] in place: query i sees keys
+ * 0 .. i + (sk - sq); the masked keys are not read and are written as 0. */
+int fence_softmax_causal(float* x, int64_t heads, int sq, int sk,
+                         hipStream_t stream);
+
+/* Q8_0 embedding gather: out [tokens][dim] = rows ids[t] (device int32) of
+ * the table [vocab][dim/32] blocks.  An id outside [0, vocab) is not read and
+ * yields a row of quiet NaN.  Bit-exact with embed_q8_0 per id. */
+int fence_embed_q8_0_gather(float* out, const void* table, int64_t vocab,
+                            const int32_t* ids, int64_t tokens, int dim,
+                            hipStream_t stream);
+
+/* Q8_0 gather fused with rms_norm (weight w[dim]) on each gathered row. */
+int fence_embed_q8_0_gather_rms_norm(float* out, const void* table,
+                                     int64_t vocab, const int32_t* ids,
+                                     int64_t tokens, int dim, const float* w,
+                                     float eps, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Host-side helpers (no device work).
+ * ------------------------------------------------------------------------ */
+
+/* inv_freq[p] = 1.0f / powf(freq_base, (float)(2p) / (float)head_dim) for
+ * p < head_dim/2 (src/kernels/ops.cuh:133), computed on the host: the RoPE
+ * kernels receive exactly these values. */
+int fence_rope_inv_freq(float* inv_freq, int head_dim, float freq_base);
+
+/* Static text for a status code. */
+const char* fence_status_string(int status);
+
+/* Library version string. */
+const char* fence_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FENCE_OPS_H */

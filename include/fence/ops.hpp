@@ -1,0 +1,71 @@
+/*
+ * fence/ops.hpp -- drop-in launchers with the reference's names, argument
+ * order and defaults (src/kernels/ops.cuh, src/kernels/gemv_q8_0.cuh), so a
+ * HIP build of the reference's model code (src/model/qwen3.cu) calls the
+ * gfx950 kernels without changing a call site: include this header where it
+ * included ops.cuh / gemv_q8_0.cuh.
+ *
+ * Like the reference launchers these return void.  The status of the last
+ * call on this host thread is kept for fence_last_status(); an invalid
+ * argument launches nothing (the reference launchers would have launched
+ * anyway and failed later, at the next synchronisation).
+ */
+#ifndef FENCE_OPS_HPP
+#define FENCE_OPS_HPP
+
+#include "fence/ops.h"
+#include "fence/q8_0_types.h"
+
+namespace fence_detail {
+inline int& last_status() {
+    thread_local int status = FENCE_SUCCESS;
+    return status;
+}
+inline void record(int status) { last_status() = status; }
+}  // namespace fence_detail
+
+/* Status of the most recent launcher call on this thread (0 = success). */
+inline int fence_last_status() { return fence_detail::last_status(); }
+
+/* src/kernels/ops.cuh:47 */
+inline void rms_norm(float* out, const float* x, const float* w, int n, float eps,
+                     hipStream_t stream = 0) {
+    fence_detail::record(fence_rms_norm(out, x, w, n, eps, stream));
+}
+
+/* src/kernels/ops.cuh:54 */
+inline void rms_norm_inplace(float* x, const float* w, int n, float eps, hipStream_t stream = 0) {
+    fence_detail::record(fence_rms_norm_inplace(x, w, n, eps, stream));
+}
+
+/* src/kernels/ops.cuh:97 */
+inline void rms_norm_per_head(float* x, const float* w, int n_heads, int head_dim, float eps,
+                              hipStream_t stream = 0) {
+    fence_detail::record(fence_rms_norm_per_head(x, w, n_heads, head_dim, eps, stream));
+}
+
+/* src/kernels/ops.cuh:169 */
+inline void apply_rope(float* q, float* k, int head_dim, int n_q_heads, int n_kv_heads, int pos,
+                       float freq_base, hipStream_t stream = 0) {
+    fence_detail::record(
+        fence_apply_rope(q, k, head_dim, n_q_heads, n_kv_heads, pos, freq_base, stream));
+}
+
+/* src/kernels/ops.cuh:197 */
+inline void silu_elementwise_mul(float* out, const float* gate, const float* up, int n,
+                                 hipStream_t stream = 0) {
+    fence_detail::record(fence_silu_elementwise_mul(out, gate, up, n, stream));
+}
+
+/* src/kernels/ops.cuh:248 */
+inline void softmax(float* x, int n, hipStream_t stream = 0) {
+    fence_detail::record(fence_softmax(x, n, stream));
+}
+
+/* src/kernels/gemv_q8_0.cuh:31 */
+inline void embed_q8_0(float* d_out, const block_q8_0* d_weight, int token_id, int dim,
+                       hipStream_t stream = 0) {
+    fence_detail::record(fence_embed_q8_0(d_out, d_weight, token_id, dim, stream));
+}
+
+#endif /* FENCE_OPS_HPP */

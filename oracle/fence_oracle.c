@@ -1,0 +1,253 @@
+/*
+ * fence_oracle.c -- scalar CPU restatement of Fence's fused per-layer ops.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels, never part of
+ * the product path.  Build: see oracle/Makefile (gcc -O2 -ffp-contract=off,
+ * no fast-math).  Numerics conventions are stated in fence_oracle.h.
+ */
+#include "fence_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+static float bits_to_f32(uint32_t b) {
+    float f;
+    memcpy(&f, &b, sizeof f);
+    return f;
+}
+
+static uint32_t f32_to_bits(float f) {
+    uint32_t b;
+    memcpy(&b, &f, sizeof b);
+    return b;
+}
+
+/* IEEE binary16 -> binary32, exact for every finite input.
+ * The reference decodes with __half2float (src/kernels/gemv_q8_0.cuh:27). */
+float fo_fp16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1Fu;
+    const uint32_t man = h & 0x3FFu;
+    if (exp == 0) {
+        if (man == 0) return bits_to_f32(sign);
+        /* subnormal: man * 2^-24, exactly representable in fp32 */
+        const float mag = (float)man * 0x1p-24f;
+        return bits_to_f32(sign | f32_to_bits(mag));
+    }
+    if (exp == 31) {
+        uint32_t b = sign | 0x7F800000u | (man << 13);
+        if (man) b |= 0x00400000u; /* quiet the NaN */
+        return bits_to_f32(b);
+    }
+    return bits_to_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+/* ---------------------------------------------------------------- RMSNorm */
+
+/* src/kernels/ops.cuh:17-45: ss = sum x^2; r = rsqrt(ss/n + eps);
+ * out[i] = w[i] * x[i] * r, multiplied in that order. */
+static float rms_scale(const float* x, int n, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+    return (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+}
+
+void fo_rms_norm(float* out, const float* x, const float* w, int n, float eps) {
+    const float r = rms_scale(x, n, eps);
+    for (int i = 0; i < n; ++i) out[i] = (w[i] * x[i]) * r;
+}
+
+/* src/kernels/ops.cuh:54-60 */
+void fo_rms_norm_inplace(float* x, const float* w, int n, float eps) {
+    fo_rms_norm(x, x, w, n, eps);
+}
+
+void fo_rms_norm_rows(float* out, const float* x, const float* w,
+                      int64_t rows, int n, float eps) {
+    for (int64_t r = 0; r < rows; ++r)
+        fo_rms_norm(out + r * n, x + r * n, w, n, eps);
+}
+
+/* src/kernels/ops.cuh:66-95: each head of head_dim values normalised on its
+ * own, the weight w[head_dim] shared by all heads. */
+void fo_rms_norm_per_head(float* x, const float* w, int n_heads, int head_dim,
+                          float eps) {
+    for (int h = 0; h < n_heads; ++h) {
+        float* hx = x + (int64_t)h * head_dim;
+        fo_rms_norm(hx, hx, w, head_dim, eps);
+    }
+}
+
+/* ------------------------------------------------------------------- RoPE */
+
+/* src/kernels/ops.cuh:133: freq = 1.0f / powf(base, (float)(2p) / (float)hd) */
+void fo_rope_inv_freq(float* inv_freq, int head_dim, float freq_base) {
+    for (int p = 0; p < head_dim / 2; ++p)
+        inv_freq[p] = 1.0f / powf(freq_base, (float)(2 * p) / (float)head_dim);
+}
+
+/* src/kernels/ops.cuh:133-144 (NeoX: pair (p, p+hd/2)) and the interleaved
+ * form of its comment, ops.cuh:109-113 (pair (2p, 2p+1)):
+ *   a = (float)pos * freq;  x0' = x0 cos a - x1 sin a;  x1' = x0 sin a + x1 cos a */
+void fo_rope_head(float* x, int head_dim, int pos, float freq_base, int style) {
+    const int half = head_dim / 2;
+    for (int p = 0; p < half; ++p) {
+        const float freq = 1.0f / powf(freq_base, (float)(2 * p) / (float)head_dim);
+        const float angle = (float)pos * freq;
+        const float c = cosf(angle);
+        const float s = sinf(angle);
+        const int i0 = (style == FO_ROPE_NEOX) ? p : 2 * p;
+        const int i1 = (style == FO_ROPE_NEOX) ? p + half : 2 * p + 1;
+        const float x0 = x[i0];
+        const float x1 = x[i1];
+        x[i0] = x0 * c - x1 * s;
+        x[i1] = x0 * s + x1 * c;
+    }
+}
+
+/* src/kernels/ops.cuh:115-177: all q heads, then all k heads, one position */
+void fo_apply_rope(float* q, float* k, int head_dim, int n_q_heads,
+                   int n_kv_heads, int pos, float freq_base) {
+    for (int h = 0; h < n_q_heads; ++h)
+        fo_rope_head(q + (int64_t)h * head_dim, head_dim, pos, freq_base, FO_ROPE_NEOX);
+    for (int h = 0; h < n_kv_heads; ++h)
+        fo_rope_head(k + (int64_t)h * head_dim, head_dim, pos, freq_base, FO_ROPE_NEOX);
+}
+
+static int token_pos(const int32_t* positions, int pos0, int64_t t) {
+    return positions ? positions[t] : pos0 + (int)t;
+}
+
+void fo_rope_rows(float* q, float* k, int64_t tokens, int n_q_heads,
+                  int n_kv_heads, int head_dim, const int32_t* positions,
+                  int pos0, float freq_base, int style) {
+    const int64_t qrow = (int64_t)n_q_heads * head_dim;
+    const int64_t krow = (int64_t)n_kv_heads * head_dim;
+    for (int64_t t = 0; t < tokens; ++t) {
+        const int pos = token_pos(positions, pos0, t);
+        for (int h = 0; h < n_q_heads; ++h)
+            fo_rope_head(q + t * qrow + (int64_t)h * head_dim, head_dim, pos,
+                         freq_base, style);
+        if (k)
+            for (int h = 0; h < n_kv_heads; ++h)
+                fo_rope_head(k + t * krow + (int64_t)h * head_dim, head_dim, pos,
+                             freq_base, style);
+    }
+}
+
+/* ----------------------------------------------------------------- SwiGLU */
+
+/* src/kernels/ops.cuh:189-194: out = (g / (1 + expf(-g))) * up */
+void fo_silu_elementwise_mul(float* out, const float* gate, const float* up,
+                             int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = gate[i];
+        const float silu_g = g / (1.0f + expf(-g));
+        out[i] = silu_g * up[i];
+    }
+}
+
+/* ---------------------------------------------------------------- softmax */
+
+/* src/kernels/ops.cuh:207-246 (and the decode form ops.cuh:357-391):
+ * m = max(-1e30f, x_i); e_i = expf(x_i - m); x_i = e_i * (1.0f / sum e). */
+static void softmax_row(float* x, int n_valid) {
+    float m = -1e30f;
+    for (int i = 0; i < n_valid; ++i) m = fmaxf(m, x[i]);
+    double s = 0.0;
+    for (int i = 0; i < n_valid; ++i) {
+        const float e = expf(x[i] - m);
+        x[i] = e;
+        s += (double)e;
+    }
+    const float inv = 1.0f / (float)s;
+    for (int i = 0; i < n_valid; ++i) x[i] *= inv;
+}
+
+void fo_softmax(float* x, int n) { softmax_row(x, n); }
+
+void fo_softmax_rows(float* x, int64_t rows, int n, int64_t ld) {
+    for (int64_t r = 0; r < rows; ++r) softmax_row(x + r * ld, n);
+}
+
+void fo_softmax_causal(float* x, int64_t heads, int sq, int sk) {
+    for (int64_t h = 0; h < heads; ++h) {
+        for (int i = 0; i < sq; ++i) {
+            float* row = x + (h * sq + i) * (int64_t)sk;
+            int valid = i + 1 + (sk - sq);
+            if (valid < 0) valid = 0;
+            if (valid > sk) valid = sk;
+            softmax_row(row, valid);
+            for (int j = valid; j < sk; ++j) row[j] = 0.0f;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------- Q8_0 */
+
+/* src/kernels/gemv_q8_0.cuh:12-29 with the block layout of
+ * src/kernels/q8_0_types.h:10-15: out[i] = half2float(d[i/32]) * qs[i/32][i%32] */
+void fo_embed_q8_0(float* out, const uint8_t* table, int token_id, int dim) {
+    const int nb = dim / FO_QK8_0;
+    const uint8_t* row = table + (int64_t)token_id * nb * FO_Q8_0_BLOCK_BYTES;
+    for (int i = 0; i < dim; ++i) {
+        const uint8_t* blk = row + (i / FO_QK8_0) * FO_Q8_0_BLOCK_BYTES;
+        const uint16_t dbits = (uint16_t)(blk[0] | ((uint16_t)blk[1] << 8));
+        const float d = fo_fp16_to_f32(dbits);
+        const int8_t q = (int8_t)blk[2 + i % FO_QK8_0];
+        out[i] = d * (float)q;
+    }
+}
+
+int64_t fo_embed_q8_0_gather(float* out, const uint8_t* table, int64_t vocab,
+                             const int32_t* ids, int64_t tokens, int dim) {
+    int64_t bad = 0;
+    for (int64_t t = 0; t < tokens; ++t) {
+        float* o = out + t * dim;
+        if (ids[t] < 0 || ids[t] >= vocab) {
+            for (int i = 0; i < dim; ++i) o[i] = bits_to_f32(0x7FC00000u);
+            ++bad;
+            continue;
+        }
+        fo_embed_q8_0(o, table, ids[t], dim);
+    }
+    return bad;
+}
+
+int64_t fo_embed_q8_0_gather_rms_norm(float* out, const uint8_t* table,
+                                      int64_t vocab, const int32_t* ids,
+                                      int64_t tokens, int dim, const float* w,
+                                      float eps) {
+    const int64_t bad = fo_embed_q8_0_gather(out, table, vocab, ids, tokens, dim);
+    for (int64_t t = 0; t < tokens; ++t) {
+        float* o = out + t * dim;
+        fo_rms_norm(o, o, w, dim, eps);
+    }
+    return bad;
+}
+
+/* ------------------------------------------------------ fused compositions */
+
+void fo_qk_norm_rope(float* q, float* k, const float* wq, const float* wk,
+                     int64_t tokens, int n_q_heads, int n_kv_heads,
+                     int head_dim, float eps, const int32_t* positions,
+                     int pos0, float freq_base, int style) {
+    const int64_t qrow = (int64_t)n_q_heads * head_dim;
+    const int64_t krow = (int64_t)n_kv_heads * head_dim;
+    for (int64_t t = 0; t < tokens; ++t) {
+        fo_rms_norm_per_head(q + t * qrow, wq, n_q_heads, head_dim, eps);
+        if (k) fo_rms_norm_per_head(k + t * krow, wk, n_kv_heads, head_dim, eps);
+    }
+    fo_rope_rows(q, k, tokens, n_q_heads, n_kv_heads, head_dim, positions, pos0,
+                 freq_base, style);
+}
+
+void fo_rms_norm_rope(float* out, const float* x, const float* w, float* k,
+                      int64_t tokens, int n_q_heads, int n_kv_heads,
+                      int head_dim, float eps, const int32_t* positions,
+                      int pos0, float freq_base, int style) {
+    const int n = n_q_heads * head_dim;
+    fo_rms_norm_rows(out, x, w, tokens, n, eps);
+    fo_rope_rows(out, k, tokens, n_q_heads, n_kv_heads, head_dim, positions, pos0,
+                 freq_base, style);
+}

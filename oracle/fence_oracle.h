@@ -1,0 +1,115 @@
+/*
+ * fence_oracle.h -- scalar CPU restatement of Fence's fused per-layer ops.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP kernels
+ * in the product library (libfence_ops.so).  Only the tests, the smoke check
+ * and the CPU-baseline leg of bench.py may load it; the product path never
+ * calls it and never falls back to it.
+ *
+ * Each function cites the reference launcher/kernel it restates
+ * (paths are relative to the reference repository root).
+ *
+ * Numerics (deliberate, documented choices):
+ *   - fp32 element arithmetic, compiled with -ffp-contract=off and without
+ *     fast-math, so every product and sum is rounded exactly once as written;
+ *   - row reductions (sum of squares, sum of exponentials) accumulate in
+ *     double: the reference's fp32 shared-memory tree order is not
+ *     reproducible and double is closer to the exact value;
+ *   - transcendentals are glibc powf / sinf / cosf / expf (the reference is
+ *     built with --use_fast_math, whose approximate intrinsics cannot be run
+ *     here; the parity target is the formula, not that binary);
+ *   - fp16 is decoded by an explicit bit routine (signalling NaNs are quieted,
+ *     as IEEE-754 conversion and the x86 F16C / AMD v_cvt_f32_f16
+ *     instructions do).
+ *
+ * Parity pinning for every function is listed in the tests
+ * (tests/oracle_checks.py); the mutation tests plant mistakes in a copy of
+ * this oracle and require that those checks catch each one.
+ */
+#ifndef FENCE_ORACLE_H
+#define FENCE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Q8_0 block: fp16 scale followed by 32 int8 values, 34 bytes, packed.
+ * Follows src/kernels/q8_0_types.h:8-17. */
+#define FO_QK8_0 32
+#define FO_Q8_0_BLOCK_BYTES 34
+
+enum { FO_ROPE_NEOX = 0, FO_ROPE_INTERLEAVED = 1 };
+
+float fo_fp16_to_f32(uint16_t h);
+
+/* a1: src/kernels/ops.cuh:17-51 */
+void fo_rms_norm(float* out, const float* x, const float* w, int n, float eps);
+/* a2: src/kernels/ops.cuh:54-60 (out aliases x) */
+void fo_rms_norm_inplace(float* x, const float* w, int n, float eps);
+/* a1 applied to `rows` consecutive rows of length n (prefill composition) */
+void fo_rms_norm_rows(float* out, const float* x, const float* w,
+                      int64_t rows, int n, float eps);
+/* a3: src/kernels/ops.cuh:66-103 */
+void fo_rms_norm_per_head(float* x, const float* w, int n_heads, int head_dim,
+                          float eps);
+
+/* inverse frequency of pair p: src/kernels/ops.cuh:133 */
+void fo_rope_inv_freq(float* inv_freq, int head_dim, float freq_base);
+/* rotate one head in place at one position.
+ * NeoX pairs (p, p+hd/2): src/kernels/ops.cuh:133-144;
+ * interleaved pairs (2p, 2p+1): comment src/kernels/ops.cuh:109-113. */
+void fo_rope_head(float* x, int head_dim, int pos, float freq_base, int style);
+/* a4: src/kernels/ops.cuh:115-177 (NeoX, Q and K in one call) */
+void fo_apply_rope(float* q, float* k, int head_dim, int n_q_heads,
+                   int n_kv_heads, int pos, float freq_base);
+/* a4/a5 over tokens: q [tokens][n_q_heads][hd], k [tokens][n_kv_heads][hd];
+ * position of token t = positions ? positions[t] : pos0 + t. */
+void fo_rope_rows(float* q, float* k, int64_t tokens, int n_q_heads,
+                  int n_kv_heads, int head_dim, const int32_t* positions,
+                  int pos0, float freq_base, int style);
+
+/* a6: src/kernels/ops.cuh:183-202 (out may alias gate) */
+void fo_silu_elementwise_mul(float* out, const float* gate, const float* up,
+                             int64_t n);
+
+/* a9: src/kernels/ops.cuh:207-251, in place */
+void fo_softmax(float* x, int n);
+/* a9 on `rows` rows of length n, row stride ld (decode score rows,
+ * src/kernels/ops.cuh:357-391 with seq_len = n, stride max_ctx) */
+void fo_softmax_rows(float* x, int64_t rows, int n, int64_t ld);
+/* causal softmax over [heads][sq][sk]: query i sees keys 0..i+(sk-sq);
+ * masked keys are written as exactly 0 (== expf(-inf - m)). */
+void fo_softmax_causal(float* x, int64_t heads, int sq, int sk);
+
+/* a10: src/kernels/gemv_q8_0.cuh:12-36 */
+void fo_embed_q8_0(float* out, const uint8_t* table, int token_id, int dim);
+/* a12: one a10 per token; an id outside [0,vocab) yields a row of quiet NaN.
+ * Returns the number of out-of-range ids. */
+int64_t fo_embed_q8_0_gather(float* out, const uint8_t* table, int64_t vocab,
+                             const int32_t* ids, int64_t tokens, int dim);
+/* a12 then a1 on each gathered row */
+int64_t fo_embed_q8_0_gather_rms_norm(float* out, const uint8_t* table,
+                                      int64_t vocab, const int32_t* ids,
+                                      int64_t tokens, int dim, const float* w,
+                                      float eps);
+
+/* a7: per-head RMSNorm of q (weight wq[hd]) and k (wk[hd]) then RoPE,
+ * per token (src/model/qwen3.cu:293-299 composed). */
+void fo_qk_norm_rope(float* q, float* k, const float* wq, const float* wk,
+                     int64_t tokens, int n_q_heads, int n_kv_heads,
+                     int head_dim, float eps, const int32_t* positions,
+                     int pos0, float freq_base, int style);
+/* a8: out_t = RoPE(rms_norm(x_t, w)) viewed as [n_q_heads][hd]; k gets RoPE
+ * only (apply_rope's q+k contract, src/kernels/ops.cuh:169). */
+void fo_rms_norm_rope(float* out, const float* x, const float* w, float* k,
+                      int64_t tokens, int n_q_heads, int n_kv_heads,
+                      int head_dim, float eps, const int32_t* positions,
+                      int pos0, float freq_base, int style);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FENCE_ORACLE_H */

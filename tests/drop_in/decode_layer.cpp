@@ -1,0 +1,193 @@
+// decode_layer.cpp -- the drop-in check.  One decode step's hot-path calls,
+// made through the reference's own launcher names (include/fence/ops.hpp) in
+// the order src/model/qwen3.cu makes them (forward :246, forward_attention
+// :274-299, gqa softmax :357-391, forward_mlp :324-332, final norm :257), at
+// Qwen3-4B shapes, each output checked against the CPU oracle.
+// Prints one PASS/FAIL line per check and exits with the number of failures.
+#include "fence/ops.hpp"
+#include "fence_oracle.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#define HIP_CHECK(call)                                                                    \
+    do {                                                                                   \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess) {                                                            \
+            std::fprintf(stderr, "HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, \
+                         __LINE__);                                                        \
+            std::exit(100);                                                                \
+        }                                                                                  \
+    } while (0)
+
+namespace {
+
+struct Rng {  // splitmix64 + Box-Muller
+    uint64_t s;
+    uint64_t next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    double uniform() { return (next() >> 11) * (1.0 / 9007199254740992.0); }
+    float normal(double mean = 0.0, double std = 1.0) {
+        const double u1 = uniform() + 1e-300, u2 = uniform();
+        return static_cast<float>(mean + std * std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+    }
+};
+
+int g_pass = 0, g_fail = 0;
+
+void report(const char* name, bool ok, double rel, double maxabs) {
+    std::printf("%s %-44s rel %.3e  max-abs %.3e\n", ok ? "PASS" : "FAIL", name, rel, maxabs);
+    (ok ? g_pass : g_fail)++;
+}
+
+// per row: max|got-ref| <= 1e-5 * max|ref|
+void check_rows(const char* name, const std::vector<float>& got, const std::vector<float>& ref, int row) {
+    double worst = 0.0, maxabs = 0.0;
+    bool ok = got.size() == ref.size();
+    for (size_t r0 = 0; ok && r0 < ref.size(); r0 += row) {
+        double d = 0.0, m = 0.0;
+        for (int i = 0; i < row; ++i) {
+            d = std::fmax(d, std::fabs((double)got[r0 + i] - (double)ref[r0 + i]));
+            m = std::fmax(m, std::fabs((double)ref[r0 + i]));
+        }
+        if (!(d <= 1e-5 * m)) ok = false;
+        worst = std::fmax(worst, m > 0 ? d / m : d);
+        maxabs = std::fmax(maxabs, d);
+    }
+    report(name, ok, worst, maxabs);
+}
+
+void check_bits(const char* name, const std::vector<float>& got, const std::vector<float>& ref) {
+    bool ok = got.size() == ref.size() && std::memcmp(got.data(), ref.data(), got.size() * 4) == 0;
+    report(name, ok, 0.0, 0.0);
+}
+
+struct Dev {
+    float* p = nullptr;
+    size_t n = 0;
+    explicit Dev(size_t n_) : n(n_) { HIP_CHECK(hipMalloc(&p, n * sizeof(float))); }
+    ~Dev() { (void)hipFree(p); }
+    void put(const std::vector<float>& h) { HIP_CHECK(hipMemcpy(p, h.data(), n * 4, hipMemcpyHostToDevice)); }
+    std::vector<float> get() const {
+        std::vector<float> h(n);
+        HIP_CHECK(hipDeviceSynchronize());
+        HIP_CHECK(hipMemcpy(h.data(), p, n * 4, hipMemcpyDeviceToHost));
+        return h;
+    }
+};
+
+std::vector<float> normals(Rng& r, size_t n, double mean = 0.0, double std = 1.0) {
+    std::vector<float> v(n);
+    for (auto& x : v) x = r.normal(mean, std);
+    return v;
+}
+
+}  // namespace
+
+int main() {
+    // Qwen3-4B (src/model/qwen3.h:19-44 defaults; rope base as in configs[0])
+    const int E = 2560, NQ = 32, NKV = 8, HD = 128, FF = 9728, V = 151936;
+    const float eps = 1e-6f, base = 1e6f;
+    Rng rng{20240601};
+    const int pos = static_cast<int>(rng.uniform() * 4096);
+    const int token = 9707;
+
+    // Q8_0 token embedding: fp16 scale |N(0,0.02)|/127 (RNE via __half), int8 in [-127,127]
+    const size_t nb = E / 32;
+    std::vector<block_q8_0> table(static_cast<size_t>(V) * nb);
+    for (auto& b : table) {
+        b.d = __float2half(std::fabs(rng.normal(0.0, 0.02)) / 127.0f);
+        for (auto& q : b.qs) q = static_cast<int8_t>(static_cast<int>(rng.uniform() * 255.0) - 127);
+    }
+    block_q8_0* d_table = nullptr;
+    HIP_CHECK(hipMalloc(&d_table, table.size() * sizeof(block_q8_0)));
+    HIP_CHECK(hipMemcpy(d_table, table.data(), table.size() * sizeof(block_q8_0), hipMemcpyHostToDevice));
+
+    Dev hidden(E), normed(E), q(NQ * HD), k(NKV * HD), gate(FF), up(FF), scores(NQ * 4096);
+    Dev attn_norm(E), ffn_norm(E), out_norm(E), q_norm(HD), k_norm(HD);
+    auto w_attn = normals(rng, E, 1.0, 0.1), w_ffn = normals(rng, E, 1.0, 0.1), w_out = normals(rng, E, 1.0, 0.1);
+    auto w_q = normals(rng, HD, 1.0, 0.1), w_k = normals(rng, HD, 1.0, 0.1);
+    attn_norm.put(w_attn); ffn_norm.put(w_ffn); out_norm.put(w_out); q_norm.put(w_q); k_norm.put(w_k);
+
+    // 1. embed (qwen3.cu:246)
+    embed_q8_0(hidden.p, d_table, token, E);
+    std::vector<float> h_ref(E);
+    fo_embed_q8_0(h_ref.data(), reinterpret_cast<const uint8_t*>(table.data()), token, E);
+    const auto h = hidden.get();
+    check_bits("embed_q8_0 (bit-exact)", h, h_ref);
+    embed_q8_0(normed.p, d_table, V - 1, E);
+    std::vector<float> last_ref(E);
+    fo_embed_q8_0(last_ref.data(), reinterpret_cast<const uint8_t*>(table.data()), V - 1, E);
+    check_bits("embed_q8_0 last row (bit-exact)", normed.get(), last_ref);
+
+    // 2. attention RMSNorm (qwen3.cu:274)
+    rms_norm(normed.p, hidden.p, attn_norm.p, E, eps);
+    std::vector<float> n_ref(E);
+    fo_rms_norm(n_ref.data(), h.data(), w_attn.data(), E, eps);
+    check_rows("rms_norm(attn)", normed.get(), n_ref, E);
+
+    // 3. QK-norm (qwen3.cu:293-294) on synthetic projections
+    auto hq = normals(rng, NQ * HD), hk = normals(rng, NKV * HD);
+    q.put(hq); k.put(hk);
+    rms_norm_per_head(q.p, q_norm.p, NQ, HD, eps);
+    rms_norm_per_head(k.p, k_norm.p, NKV, HD, eps);
+    fo_rms_norm_per_head(hq.data(), w_q.data(), NQ, HD, eps);
+    fo_rms_norm_per_head(hk.data(), w_k.data(), NKV, HD, eps);
+    check_rows("rms_norm_per_head(q)", q.get(), hq, HD);
+    check_rows("rms_norm_per_head(k)", k.get(), hk, HD);
+
+    // 4. RoPE (qwen3.cu:299), continuing from the device's normalised q/k
+    auto dq = q.get(), dk = k.get();
+    apply_rope(q.p, k.p, HD, NQ, NKV, pos, base);
+    fo_apply_rope(dq.data(), dk.data(), HD, NQ, NKV, pos, base);
+    check_rows("apply_rope(q) NeoX", q.get(), dq, HD);
+    check_rows("apply_rope(k) NeoX", k.get(), dk, HD);
+
+    // 5. the attention softmax over pos+1 scores of one head (ops.cuh:357-391)
+    auto hs = normals(rng, pos + 1, 0.0, 3.0 / std::sqrt(128.0));
+    std::vector<float> srow(hs);
+    srow.resize(4096 * NQ, 0.0f);
+    scores.put(srow);
+    softmax(scores.p, pos + 1);
+    fo_softmax(hs.data(), pos + 1);
+    auto sg = scores.get();
+    sg.resize(pos + 1);
+    check_rows("softmax(pos+1)", sg, hs, pos + 1);
+
+    // 6. FFN RMSNorm and SwiGLU with out aliasing gate (qwen3.cu:324, :332)
+    rms_norm(normed.p, hidden.p, ffn_norm.p, E, eps);
+    fo_rms_norm(n_ref.data(), h.data(), w_ffn.data(), E, eps);
+    check_rows("rms_norm(ffn)", normed.get(), n_ref, E);
+    auto hg = normals(rng, FF), hu = normals(rng, FF);
+    gate.put(hg); up.put(hu);
+    silu_elementwise_mul(gate.p, gate.p, up.p, FF);
+    fo_silu_elementwise_mul(hg.data(), hg.data(), hu.data(), FF);
+    check_rows("silu_elementwise_mul(out == gate)", gate.get(), hg, FF);
+
+    // 7. final norm in place (qwen3.cu:257)
+    rms_norm_inplace(hidden.p, out_norm.p, E, eps);
+    std::vector<float> f_ref(h);
+    fo_rms_norm_inplace(f_ref.data(), w_out.data(), E, eps);
+    check_rows("rms_norm_inplace(output)", hidden.get(), f_ref, E);
+
+    // 8. error behaviour: a null pointer launches nothing and leaves EINVAL
+    rms_norm(nullptr, hidden.p, out_norm.p, E, eps);
+    report("invalid launch reports EINVAL", fence_last_status() == FENCE_ERROR_INVALID_VALUE, 0, 0);
+    rms_norm(normed.p, hidden.p, out_norm.p, E, eps);
+    report("valid launch reports success", fence_last_status() == FENCE_SUCCESS, 0, 0);
+
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipFree(d_table));
+    std::printf("%d/%d passed\n", g_pass, g_pass + g_fail);
+    return g_fail;
+}

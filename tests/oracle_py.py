@@ -1,0 +1,224 @@
+"""numpy-facing wrapper of the CPU oracle (oracle/libfence_oracle.so).
+
+Test infrastructure: only the tests, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py use it, as the checker.  Every function copies
+its inputs and returns fresh outputs; in-place reference ops are exposed as
+functions returning the updated array.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_PATH = os.path.join(ROOT, "oracle", "libfence_oracle.so")
+
+NEOX = 0
+INTERLEAVED = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+_SIGS = {
+    "fo_fp16_to_f32": ((ctypes.c_uint16,), ctypes.c_float),
+    "fo_rms_norm": ((_P, _P, _P, _I, _F), None),
+    "fo_rms_norm_inplace": ((_P, _P, _I, _F), None),
+    "fo_rms_norm_rows": ((_P, _P, _P, _L, _I, _F), None),
+    "fo_rms_norm_per_head": ((_P, _P, _I, _I, _F), None),
+    "fo_rope_inv_freq": ((_P, _I, _F), None),
+    "fo_rope_head": ((_P, _I, _I, _F, _I), None),
+    "fo_apply_rope": ((_P, _P, _I, _I, _I, _I, _F), None),
+    "fo_rope_rows": ((_P, _P, _L, _I, _I, _I, _P, _I, _F, _I), None),
+    "fo_silu_elementwise_mul": ((_P, _P, _P, _L), None),
+    "fo_softmax": ((_P, _I), None),
+    "fo_softmax_rows": ((_P, _L, _I, _L), None),
+    "fo_softmax_causal": ((_P, _L, _I, _I), None),
+    "fo_embed_q8_0": ((_P, _P, _I, _I), None),
+    "fo_embed_q8_0_gather": ((_P, _P, _L, _P, _L, _I), ctypes.c_int64),
+    "fo_embed_q8_0_gather_rms_norm": ((_P, _P, _L, _P, _L, _I, _P, _F), ctypes.c_int64),
+    "fo_qk_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
+    "fo_rms_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
+}
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32).copy()
+
+
+class Oracle:
+    """One loaded oracle library (the real one, or a mutant in the mutation tests)."""
+
+    def __init__(self, path: str = ORACLE_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is missing: run `make -C oracle`")
+        self.path = path
+        self.lib = ctypes.CDLL(path)
+        for name, (argtypes, restype) in _SIGS.items():
+            fn = getattr(self.lib, name)
+            fn.argtypes = list(argtypes)
+            fn.restype = restype
+
+    # fp16 ------------------------------------------------------------------
+    def fp16_to_f32(self, bits: int) -> float:
+        return self.lib.fo_fp16_to_f32(bits)
+
+    def fp16_to_f32_all(self) -> np.ndarray:
+        """Oracle decode of all 65536 binary16 patterns, as fp32 bit patterns."""
+        out = np.empty(65536, dtype=np.float32)
+        for b in range(65536):
+            out[b] = self.lib.fo_fp16_to_f32(b)
+        return out.view(np.uint32)
+
+    # RMSNorm ---------------------------------------------------------------
+    def rms_norm(self, x, w, eps):
+        x = _f32(x); w = _f32(w); out = np.empty_like(x)
+        self.lib.fo_rms_norm(_ptr(out), _ptr(x), _ptr(w), x.size, eps)
+        return out
+
+    def rms_norm_inplace(self, x, w, eps):
+        x = _f32(x); w = _f32(w)
+        self.lib.fo_rms_norm_inplace(_ptr(x), _ptr(w), x.size, eps)
+        return x
+
+    def rms_norm_rows(self, x, w, eps):
+        x = _f32(x); w = _f32(w); out = np.empty_like(x)
+        rows, n = x.shape
+        self.lib.fo_rms_norm_rows(_ptr(out), _ptr(x), _ptr(w), rows, n, eps)
+        return out
+
+    def rms_norm_per_head(self, x, w, eps):
+        """x [n_heads, head_dim]"""
+        x = _f32(x); w = _f32(w)
+        n_heads, hd = x.shape
+        self.lib.fo_rms_norm_per_head(_ptr(x), _ptr(w), n_heads, hd, eps)
+        return x
+
+    # RoPE ------------------------------------------------------------------
+    def rope_inv_freq(self, head_dim, base):
+        out = np.empty(head_dim // 2, dtype=np.float32)
+        self.lib.fo_rope_inv_freq(_ptr(out), head_dim, base)
+        return out
+
+    def rope_head(self, x, pos, base, style):
+        x = _f32(x)
+        self.lib.fo_rope_head(_ptr(x), x.size, pos, base, style)
+        return x
+
+    def apply_rope(self, q, k, pos, base):
+        """q [nq, hd], k [nkv, hd]; NeoX, one position."""
+        q = _f32(q); k = _f32(k)
+        self.lib.fo_apply_rope(_ptr(q), _ptr(k), q.shape[1], q.shape[0], k.shape[0], pos, base)
+        return q, k
+
+    def rope_rows(self, q, k, positions, pos0, base, style):
+        """q [T, nq, hd], k [T, nkv, hd] or None."""
+        q = _f32(q); k = None if k is None else _f32(k)
+        T, nq, hd = q.shape
+        nkv = 0 if k is None else k.shape[1]
+        pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.int32)
+        self.lib.fo_rope_rows(_ptr(q), _ptr(k), T, nq, nkv, hd, _ptr(pos), pos0, base, style)
+        return q, k
+
+    # SwiGLU ----------------------------------------------------------------
+    def silu_mul(self, gate, up):
+        g = _f32(gate); u = _f32(up); out = np.empty_like(g)
+        self.lib.fo_silu_elementwise_mul(_ptr(out), _ptr(g), _ptr(u), g.size)
+        return out
+
+    # softmax ---------------------------------------------------------------
+    def softmax(self, x):
+        x = _f32(x)
+        self.lib.fo_softmax(_ptr(x), x.size)
+        return x
+
+    def softmax_rows(self, x, n=None):
+        """x [rows, ld]; softmax over the first n columns of each row."""
+        x = _f32(x)
+        rows, ld = x.shape
+        self.lib.fo_softmax_rows(_ptr(x), rows, ld if n is None else n, ld)
+        return x
+
+    def softmax_causal(self, x):
+        """x [heads, sq, sk]"""
+        x = _f32(x)
+        h, sq, sk = x.shape
+        self.lib.fo_softmax_causal(_ptr(x), h, sq, sk)
+        return x
+
+    # Q8_0 ------------------------------------------------------------------
+    def embed_q8_0(self, table_bytes, token_id, dim):
+        t = np.ascontiguousarray(table_bytes, dtype=np.uint8)
+        out = np.empty(dim, dtype=np.float32)
+        self.lib.fo_embed_q8_0(_ptr(out), _ptr(t), token_id, dim)
+        return out
+
+    def embed_q8_0_gather(self, table_bytes, vocab, ids, dim):
+        t = np.ascontiguousarray(table_bytes, dtype=np.uint8)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty((ids.size, dim), dtype=np.float32)
+        bad = self.lib.fo_embed_q8_0_gather(_ptr(out), _ptr(t), vocab, _ptr(ids), ids.size, dim)
+        return out, bad
+
+    def embed_q8_0_gather_rms_norm(self, table_bytes, vocab, ids, dim, w, eps):
+        t = np.ascontiguousarray(table_bytes, dtype=np.uint8)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        w = _f32(w)
+        out = np.empty((ids.size, dim), dtype=np.float32)
+        bad = self.lib.fo_embed_q8_0_gather_rms_norm(_ptr(out), _ptr(t), vocab, _ptr(ids), ids.size,
+                                                     dim, _ptr(w), eps)
+        return out, bad
+
+    # fused -----------------------------------------------------------------
+    def qk_norm_rope(self, q, k, wq, wk, eps, positions, pos0, base, style):
+        q = _f32(q); k = None if k is None else _f32(k)
+        wq = _f32(wq); wk = None if wk is None else _f32(wk)
+        T, nq, hd = q.shape
+        nkv = 0 if k is None else k.shape[1]
+        pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.int32)
+        self.lib.fo_qk_norm_rope(_ptr(q), _ptr(k), _ptr(wq), _ptr(wk), T, nq, nkv, hd, eps,
+                                 _ptr(pos), pos0, base, style)
+        return q, k
+
+    def rms_norm_rope(self, x, w, k, n_q_heads, head_dim, eps, positions, pos0, base, style):
+        """x [T, nq*hd] -> out [T, nq*hd]; k [T, nkv, hd] or None (RoPE only)."""
+        x = _f32(x); w = _f32(w); k = None if k is None else _f32(k)
+        T = x.shape[0]
+        nkv = 0 if k is None else k.shape[1]
+        out = np.empty_like(x)
+        pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.int32)
+        self.lib.fo_rms_norm_rope(_ptr(out), _ptr(x), _ptr(w), _ptr(k), T, n_q_heads, nkv, head_dim,
+                                  eps, _ptr(pos), pos0, base, style)
+        return out, k
+
+
+# ------------------------------------------------------------ data helpers
+
+def make_q8_0_table(rng: np.random.Generator, vocab: int, dim: int) -> np.ndarray:
+    """Synthetic Q8_0 table [vocab, dim/32 * 34] bytes: fp16 scale
+    RNE(|N(0,0.02)|/127) then 32 int8 uniform in [-127, 127]."""
+    nb = dim // 32
+    d = (np.abs(rng.standard_normal((vocab, nb))) * 0.02 / 127.0).astype(np.float16)
+    qs = rng.integers(-127, 128, size=(vocab, nb, 32), dtype=np.int8)
+    blocks = np.empty((vocab, nb, 34), dtype=np.uint8)
+    blocks[:, :, 0:2] = d.view(np.uint8).reshape(vocab, nb, 2)
+    blocks[:, :, 2:] = qs.view(np.uint8)
+    return blocks.reshape(vocab, nb * 34)
+
+
+def q8_0_dequant_numpy(table_bytes: np.ndarray, ids, dim: int) -> np.ndarray:
+    """Independent dequant via numpy's float16 -> float32 conversion (not the
+    oracle's bit routine).  Products of an fp16 and an int8 are exact in fp32."""
+    nb = dim // 32
+    rows = table_bytes[np.asarray(ids)].reshape(-1, nb, 34)
+    d = rows[:, :, 0:2].copy().view(np.float16).astype(np.float32)  # [T, nb, 1]
+    q = rows[:, :, 2:].copy().view(np.int8).astype(np.float32)      # [T, nb, 32]
+    with np.errstate(invalid="ignore"):  # inf scale * 0 -> NaN, as in fp32
+        return (d * q).reshape(-1, dim)

@@ -1,0 +1,102 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/fence/ops.h declares with the argument count the Python binding
+uses, rejects invalid arguments with EINVAL before touching the device, and
+its host-side RoPE frequencies equal the oracle's bit for bit."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import fence_ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fence", "ops.h")
+EINVAL = fence_ops.EINVAL
+BAD = 0x1002  # a non-null address that is not 4-byte aligned; never dereferenced
+
+
+def header_declarations():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[\w\s\*]+?\b(fence_\w+)\s*\(([^)]*)\)\s*;", text, re.M):
+        args = m.group(2).strip()
+        decls[m.group(1)] = 0 if args in ("", "void") else len(args.split(","))
+    return decls
+
+
+def test_header_declares_and_library_exports_everything(fence):
+    decls = header_declarations()
+    assert len(decls) >= 19
+    lib = fence.lib()
+    for name, nargs in decls.items():
+        assert hasattr(lib, name), f"{name} declared in ops.h but not exported"
+        assert name in fence_ops.SIGNATURES, f"{name} missing from the Python binding"
+        assert len(fence_ops.SIGNATURES[name]) == nargs, f"{name}: argument count differs"
+    assert set(fence_ops.SIGNATURES) == set(decls)
+
+
+def test_version_and_status_strings(fence):
+    assert "gfx950" in fence.version()
+    assert fence.status_string(0) == "success"
+    assert "invalid" in fence.status_string(EINVAL)
+
+
+def _raw(name):
+    return getattr(fence_ops.lib(), name)
+
+
+@pytest.mark.parametrize("name,args", [
+    ("fence_rms_norm", (None, 16, 32, 8, 1e-6, None)),
+    ("fence_rms_norm", (16, 16, 32, 0, 1e-6, None)),
+    ("fence_rms_norm", (BAD, 16, 32, 8, 1e-6, None)),
+    ("fence_rms_norm_inplace", (16, None, 8, 1e-6, None)),
+    ("fence_rms_norm_rows", (16, 16, 32, -1, 8, 1e-6, None)),
+    ("fence_rms_norm_per_head", (16, None, 4, 128, 1e-6, None)),
+    ("fence_rms_norm_per_head", (16, 32, 4, 0, 1e-6, None)),
+    ("fence_apply_rope", (16, 32, 127, 4, 2, 5, 1e6, None)),      # odd head_dim
+    ("fence_apply_rope", (16, 32, 512, 4, 2, 5, 1e6, None)),      # head_dim > 256
+    ("fence_apply_rope", (16, 32, 128, 4, 2, 5, -1.0, None)),     # bad base
+    ("fence_apply_rope", (16, None, 128, 4, 2, 5, 1e6, None)),    # k null, n_kv > 0
+    ("fence_rope", (16, 32, 4, 4, 2, 128, None, 0, 1e6, 7, None)),  # bad style
+    ("fence_qk_norm_rope", (16, 32, None, 48, 4, 4, 2, 128, 1e-6, None, 0, 1e6, 0, None)),
+    ("fence_rms_norm_rope", (16, 32, None, 48, 4, 4, 2, 128, 1e-6, None, 0, 1e6, 1, None)),
+    ("fence_silu_elementwise_mul", (16, None, 32, 8, None)),
+    ("fence_silu_elementwise_mul", (16, 32, 48, -3, None)),
+    ("fence_swiglu", (16, 32, BAD, 8, None)),
+    ("fence_softmax", (None, 8, None)),
+    ("fence_softmax", (16, 0, None)),
+    ("fence_softmax_rows", (16, 4, 10, 8, None)),                 # ld < n
+    ("fence_softmax_causal", (16, 2, 0, 8, None)),
+    ("fence_embed_q8_0", (16, 32, -1, 64, None)),                 # negative id
+    ("fence_embed_q8_0", (16, 32, 3, 48, None)),                  # dim % 32 != 0
+    ("fence_embed_q8_0_gather", (16, 32, 100, None, 4, 64, None)),
+    ("fence_embed_q8_0_gather", (16, 32, 0, 48, 4, 64, None)),    # vocab 0
+    ("fence_embed_q8_0_gather_rms_norm", (16, 32, 100, 48, 4, 64, None, 1e-6, None)),
+])
+def test_invalid_arguments_rejected_on_host(fence, name, args):
+    assert _raw(name)(*args) == EINVAL
+
+
+def test_zero_sized_calls_are_no_ops(fence):
+    assert _raw("fence_rms_norm_rows")(16, 16, 32, 0, 8, 1e-6, None) == 0
+    assert _raw("fence_swiglu")(16, 32, 48, 0, None) == 0
+    assert _raw("fence_rope")(16, 32, 0, 4, 2, 128, None, 0, 1e6, 0, None) == 0
+    assert _raw("fence_softmax_causal")(16, 0, 4, 4, None) == 0
+    assert _raw("fence_embed_q8_0_gather")(16, 32, 10, 48, 0, 64, None) == 0
+
+
+@pytest.mark.parametrize("base,hd", [(1e6, 128), (5e5, 128), (5e6, 128), (1e4, 64), (1e6, 256)])
+def test_host_inv_freq_bit_exact(oracle, fence, base, hd):
+    got = np.array(fence.rope_inv_freq(hd, base), dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), oracle.rope_inv_freq(hd, base).view(np.uint32))
+    fx = np.load(os.path.join(ROOT, "tests", "golden", "inv_freq.npz"))[f"b{base:g}_hd{hd}"]
+    assert np.array_equal(got.view(np.uint32), fx.view(np.uint32))
+
+
+def test_inv_freq_rejects_bad_head_dim(fence):
+    buf = (ctypes.c_float * 256)()
+    assert _raw("fence_rope_inv_freq")(ctypes.cast(buf, ctypes.c_void_p), 127, 1e6) == EINVAL
+    assert _raw("fence_rope_inv_freq")(None, 128, 1e6) == EINVAL
