@@ -5,6 +5,7 @@
 // and every lane of a group ends with the bitwise-identical value.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -137,10 +138,28 @@ inline int hip_status(hipError_t e) {
     return e == hipSuccess ? FENCE_SUCCESS : FENCE_ERROR_HIP_BASE + static_cast<int>(e);
 }
 
+// One-shot start/stop events for the next launch on this host thread
+// (fence_time_next_launch).
+struct TimingHook {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+inline TimingHook& timing_hook() {
+    thread_local TimingHook hook;
+    return hook;
+}
+
 template <class... KArgs, class Tuple, size_t... I>
 inline int launch_impl(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
                        hipStream_t stream, Tuple& args, std::index_sequence<I...>) {
     void* ptrs[] = {static_cast<void*>(&std::get<I>(args))..., nullptr};
+    TimingHook& hook = timing_hook();
+    if (hook.start || hook.stop) {
+        const hipEvent_t a = hook.start, b = hook.stop;
+        hook = TimingHook{};
+        return hip_status(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block,
+                                             ptrs, shmem, stream, a, b, 0));
+    }
     return hip_status(hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block,
                                       ptrs, shmem, stream));
 }
@@ -153,6 +172,27 @@ inline int launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
     std::tuple<KArgs...> packed(std::forward<Args>(args)...);
     return launch_impl(kernel, grid, block, shmem, stream, packed,
                        std::index_sequence_for<KArgs...>{});
+}
+
+// Workgroup shape for a row of `items` vector items (float4s): a multiple of
+// 64 threads up to 1024 and `per_lane` items per lane (<= max_per_lane),
+// choosing the fewest idle item slots, then the fewest items per lane.
+// On MI355X shallow lanes (1-2 float4 per stream) over many waves stream
+// faster than deep ones.  Returns false if the row does not fit.
+inline bool pick_row_shape(int64_t items, int max_per_lane, unsigned* threads, int* per_lane) {
+    int64_t best_idle = -1;
+    for (int pl = 1; pl <= max_per_lane; ++pl) {
+        int64_t th = (items + pl - 1) / pl;
+        th = (th + 63) / 64 * 64;
+        if (th > 1024) continue;
+        const int64_t idle = th * pl - items;
+        if (best_idle < 0 || idle < best_idle) {
+            best_idle = idle;
+            *threads = static_cast<unsigned>(th);
+            *per_lane = pl;
+        }
+    }
+    return best_idle >= 0;
 }
 
 inline unsigned grid_1d(int64_t units, int64_t per_block, int64_t cap = 1 << 30) {

@@ -7,32 +7,40 @@
 // An 11-bit by 8-bit significand product fits fp32 exactly, so every output
 // is bit-identical to the reference formula.
 //
-// One workgroup per token: the token's row (dim/32 * 34 bytes) is copied to
-// LDS with 128-bit loads (rows are 16-byte aligned whenever dim % 256 == 0),
-// then each lane builds float4 outputs from one fp16 scale and four int8s
-// read out of LDS and writes them with coalesced 128-bit stores.  The fused
-// form keeps the row in VGPRs, reduces the sum of squares and applies
+// Each lane produces one float4 of output: block b = f/8 of the row, quarter
+// k = f%8.  It reads the block's fp16 scale and its four int8s with 2-byte
+// loads straight from global memory (the 34-byte blocks are only 2-byte
+// aligned; eight neighbouring lanes share a block, so the loads coalesce into
+// the same cache lines), converts in registers and writes a 128-bit
+// non-temporal store.  The plain gather runs a 2-D grid (token x row chunk of
+// 256 float4s) with no LDS and no barrier; the fused form runs one workgroup
+// per token, keeps the row in VGPRs, reduces the sum of squares and applies
 // rms_norm (src/kernels/ops.cuh:40-44) before the single write.
 #include "common.hpp"
 
 namespace fence {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kMaxDimVec = 16384;  // 16 float4 per lane
+constexpr int kChunk = 256;        // float4 outputs per workgroup in the plain gather
+constexpr int kMaxDimVec = 32768;  // fused form: up to 8 float4 per lane at 1024 lanes
 
-enum { kStage16 = 16, kStage2 = 2, kStage1 = 1 };
-
-__device__ __forceinline__ f4 dequant4(const uint8_t* lds_row, int f) {
-    // float4 f covers elements 4f..4f+3: block b = f/8, quarter k = f%8
-    const int b = f >> 3;
+// One float4 of a dequantised row.  BYTES: table only 1-byte aligned.
+template <bool BYTES>
+__device__ __forceinline__ f4 dequant4(const uint8_t* row, int f) {
+    const uint8_t* blk = row + 34 * (f >> 3);
     const int k = f & 7;
-    const uint8_t* blk = lds_row + 34 * b;
-    const uint16_t dbits = *reinterpret_cast<const uint16_t*>(blk);
-    const uint32_t lo = *reinterpret_cast<const uint16_t*>(blk + 2 + 4 * k);
-    const uint32_t hi = *reinterpret_cast<const uint16_t*>(blk + 4 + 4 * k);
-    const uint32_t q = lo | (hi << 16);
-    const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+    uint32_t dbits, q;
+    if constexpr (BYTES) {
+        const uint8_t* p = blk + 2 + 4 * k;
+        dbits = static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8);
+        q = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) |
+            (static_cast<uint32_t>(p[2]) << 16) | (static_cast<uint32_t>(p[3]) << 24);
+    } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+        dbits = h[0];
+        q = static_cast<uint32_t>(h[1 + 2 * k]) | (static_cast<uint32_t>(h[2 + 2 * k]) << 16);
+    }
+    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(dbits)));
     f4 v;
     v.x = d * static_cast<float>(static_cast<int8_t>(q & 0xFFu));
     v.y = d * static_cast<float>(static_cast<int8_t>((q >> 8) & 0xFFu));
@@ -41,147 +49,175 @@ __device__ __forceinline__ f4 dequant4(const uint8_t* lds_row, int f) {
     return v;
 }
 
-template <bool NORM, int MAXV>
-__global__ __launch_bounds__(kThreads) void q8_gather_vec_kernel(
-    float* out, const uint8_t* table, int64_t vocab, const int32_t* ids, int single_id,
-    int64_t tokens, int dim, const float* w, float eps, int vpt, int stage) {
-    extern __shared__ __align__(16) uint8_t row_lds[];
-    __shared__ float red[kThreads / kWave];
-    const int rb = (dim / 32) * 34;
-    const int dim4 = dim / 4;
-    for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
-        const int64_t id = ids ? static_cast<int64_t>(ids[t]) : static_cast<int64_t>(single_id);
-        float* orow = out + t * dim;
-        if (id < 0 || id >= vocab) {  // uniform: the whole workgroup takes it
-            const f4 qnan = f4(__builtin_nanf(""));
-#pragma unroll
-            for (int j = 0; j < MAXV; ++j) {
-                const int f = threadIdx.x + j * kThreads;
-                if (j < vpt && f < dim4) st4<true>(orow + 4 * f, qnan);
-            }
-            continue;
-        }
-        const uint8_t* src = table + id * rb;
-        if (stage == kStage16) {
-            for (int c = threadIdx.x; c < rb / 16; c += kThreads)
-                *reinterpret_cast<u4*>(row_lds + 16 * c) =
-                    __builtin_nontemporal_load(reinterpret_cast<const u4*>(src) + c);
-        } else if (stage == kStage2) {
-            for (int c = threadIdx.x; c < rb / 2; c += kThreads)
-                reinterpret_cast<uint16_t*>(row_lds)[c] = reinterpret_cast<const uint16_t*>(src)[c];
-        } else {
-            for (int c = threadIdx.x; c < rb; c += kThreads) row_lds[c] = src[c];
-        }
-        __syncthreads();
+template <bool VEC_OUT>
+__device__ __forceinline__ void store4(float* p, f4 v) {
+    if constexpr (VEC_OUT) {
+        st4<true>(p, v);
+    } else {
+        p[0] = v.x;
+        p[1] = v.y;
+        p[2] = v.z;
+        p[3] = v.w;
+    }
+}
 
+__device__ __forceinline__ int64_t token_id(const int32_t* ids, int single_id, int64_t t) {
+    return ids ? static_cast<int64_t>(ids[t]) : static_cast<int64_t>(single_id);
+}
+
+// grid.x = tokens (grid-stride), grid.y = row chunks of kChunk float4s.
+template <bool BYTES, bool VEC_OUT>
+__global__ __launch_bounds__(kChunk) void q8_gather_kernel(float* out, const uint8_t* table,
+                                                           int64_t vocab, const int32_t* ids,
+                                                           int single_id, int64_t tokens, int dim) {
+    const int dim4 = dim >> 2;
+    const int f = blockIdx.y * kChunk + threadIdx.x;
+    if (f >= dim4) return;
+    const int64_t rb = static_cast<int64_t>(dim / 32) * 34;
+    for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+        const int64_t id = token_id(ids, single_id, t);
+        f4 v;
+        if (id < 0 || id >= vocab) v = f4(__builtin_nanf(""));
+        else v = dequant4<BYTES>(table + id * rb, f);
+        store4<VEC_OUT>(out + t * dim + 4 * f, v);
+    }
+}
+
+// One workgroup per token; `vpt` float4s per lane.
+template <bool BYTES, int MAXV>
+__global__ __launch_bounds__(1024) void q8_gather_rms_kernel(float* out, const uint8_t* table,
+                                                             int64_t vocab, const int32_t* ids,
+                                                             int64_t tokens, int dim, const float* w,
+                                                             float eps, int vpt) {
+    __shared__ float red[16];
+    const int T = blockDim.x;
+    const int dim4 = dim >> 2;
+    const int64_t rb = static_cast<int64_t>(dim / 32) * 34;
+    for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
+        const int64_t id = ids[t];
+        float* orow = out + t * dim;
+        const bool ok = id >= 0 && id < vocab;  // uniform across the workgroup
+        const uint8_t* row = table + (ok ? id : 0) * rb;
         f4 v[MAXV];
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < MAXV; ++j) {
-            const int f = threadIdx.x + j * kThreads;
-            if (j < vpt && f < dim4) {
-                v[j] = dequant4(row_lds, f);
-                if constexpr (NORM) ss += dot4(v[j]);
+            const int f = threadIdx.x + j * T;
+            if (ok && j < vpt && f < dim4) {
+                v[j] = dequant4<BYTES>(row, f);
+                ss += dot4(v[j]);
             }
         }
-        float rs = 1.0f;
-        if constexpr (NORM) {
-            const float tot = block_reduce<kThreads / kWave>(ss, OpAdd(), red);
-            rs = rsqrtf(tot / static_cast<float>(dim) + eps);
-        }
+        const float tot = block_reduce_dyn(ss, OpAdd(), red);
+        const float rs = rsqrtf(tot / static_cast<float>(dim) + eps);
 #pragma unroll
         for (int j = 0; j < MAXV; ++j) {
-            const int f = threadIdx.x + j * kThreads;
+            const int f = threadIdx.x + j * T;
             if (j < vpt && f < dim4) {
-                f4 o = v[j];
-                if constexpr (NORM) o = (ld4<false>(w + 4 * f) * o) * rs;
+                const f4 o = ok ? (ld4<false>(w + 4 * f) * v[j]) * rs : f4(__builtin_nanf(""));
                 st4<true>(orow + 4 * f, o);
             }
         }
-        __syncthreads();  // row_lds and red[] are rewritten for the next token
+        __syncthreads();  // red[] is rewritten for the next token
     }
 }
 
-// Any alignment and dim % 32 == 0: one lane per Q8_0 block, byte reads from
-// global memory, scalar stores.  The fused form reads the row twice.
-template <bool NORM>
-__global__ __launch_bounds__(kThreads) void q8_gather_scalar_kernel(
-    float* out, const uint8_t* table, int64_t vocab, const int32_t* ids, int single_id,
-    int64_t tokens, int dim, const float* w, float eps) {
-    __shared__ float red[kThreads / kWave];
+// Any alignment of out / w and dim % 32 == 0: one lane per Q8_0 block,
+// scalar stores; reads the row twice.
+__global__ __launch_bounds__(256) void q8_gather_rms_scalar_kernel(
+    float* out, const uint8_t* table, int64_t vocab, const int32_t* ids, int64_t tokens, int dim,
+    const float* w, float eps) {
+    __shared__ float red[4];
     const int nb = dim / 32;
     for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
-        const int64_t id = ids ? static_cast<int64_t>(ids[t]) : static_cast<int64_t>(single_id);
+        const int64_t id = ids[t];
         float* orow = out + t * dim;
         if (id < 0 || id >= vocab) {
-            for (int i = threadIdx.x; i < dim; i += kThreads) orow[i] = __builtin_nanf("");
+            for (int i = threadIdx.x; i < dim; i += 256) orow[i] = __builtin_nanf("");
             continue;
         }
         const uint8_t* row = table + id * static_cast<int64_t>(nb) * 34;
-        float rs = 1.0f;
-        if constexpr (NORM) {
-            float ss = 0.0f;
-            for (int b = threadIdx.x; b < nb; b += kThreads) {
-                const uint8_t* blk = row + 34 * b;
-                const float d = static_cast<float>(
-                    __builtin_bit_cast(_Float16, static_cast<uint16_t>(blk[0] | (blk[1] << 8))));
-                for (int i = 0; i < 32; ++i) {
-                    const float v = d * static_cast<float>(static_cast<int8_t>(blk[2 + i]));
-                    ss += v * v;
-                }
-            }
-            rs = rsqrtf(block_reduce<kThreads / kWave>(ss, OpAdd(), red) / static_cast<float>(dim) + eps);
+        float ss = 0.0f;
+        for (int b = threadIdx.x; b < nb; b += 256) {
+            for (int q = 0; q < 8; ++q) ss += dot4(dequant4<true>(row, 8 * b + q));
         }
-        for (int b = threadIdx.x; b < nb; b += kThreads) {
-            const uint8_t* blk = row + 34 * b;
-            const float d = static_cast<float>(
-                __builtin_bit_cast(_Float16, static_cast<uint16_t>(blk[0] | (blk[1] << 8))));
-            for (int i = 0; i < 32; ++i) {
-                float v = d * static_cast<float>(static_cast<int8_t>(blk[2 + i]));
-                if constexpr (NORM) v = (w[32 * b + i] * v) * rs;
-                orow[32 * b + i] = v;
+        const float rs = rsqrtf(block_reduce<4>(ss, OpAdd(), red) / static_cast<float>(dim) + eps);
+        for (int b = threadIdx.x; b < nb; b += 256) {
+            for (int q = 0; q < 8; ++q) {
+                const f4 v = dequant4<true>(row, 8 * b + q);
+                const int e = 32 * b + 4 * q;
+                orow[e + 0] = (w[e + 0] * v.x) * rs;
+                orow[e + 1] = (w[e + 1] * v.y) * rs;
+                orow[e + 2] = (w[e + 2] * v.z) * rs;
+                orow[e + 3] = (w[e + 3] * v.w) * rs;
             }
         }
         __syncthreads();
     }
 }
 
-template <bool NORM, int MAXV>
-int vec_launch(float* out, const uint8_t* table, int64_t vocab, const int32_t* ids, int single_id,
-               int64_t tokens, int dim, const float* w, float eps, int vpt, int stage,
-               hipStream_t s) {
-    const unsigned grid = grid_1d(tokens, 1, 1 << 20);
-    const size_t lds = ((static_cast<size_t>(dim / 32) * 34) + 15) & ~size_t(15);
-    return launch(q8_gather_vec_kernel<NORM, MAXV>, dim3(grid), dim3(kThreads), lds, s, out, table,
-                  vocab, ids, single_id, tokens, dim, w, eps, vpt, stage);
-}
-
-template <bool NORM>
-int gather_launch(float* out, const void* table_v, int64_t vocab, const int32_t* ids,
-                  int single_id, int64_t tokens, int dim, const float* w, float eps,
-                  hipStream_t s) {
-    const uint8_t* table = static_cast<const uint8_t*>(table_v);
+int check_common(float* out, const void* table, int64_t tokens, int dim, int64_t vocab,
+                 const int32_t* ids) {
     if (!out || !table || tokens < 0 || dim <= 0 || dim % 32 != 0 || vocab <= 0)
         return FENCE_ERROR_INVALID_VALUE;
-    if (NORM && !w) return FENCE_ERROR_INVALID_VALUE;
-    if (!aligned(out, 4) || (w && !aligned(w, 4)) || (ids && !aligned(ids, 4)))
-        return FENCE_ERROR_INVALID_VALUE;
+    if (!aligned(out, 4) || (ids && !aligned(ids, 4))) return FENCE_ERROR_INVALID_VALUE;
+    return FENCE_SUCCESS;
+}
+
+int gather_launch(float* out, const void* table_v, int64_t vocab, const int32_t* ids, int single_id,
+                  int64_t tokens, int dim, hipStream_t s) {
+    const int st = check_common(out, table_v, tokens, dim, vocab, ids);
+    if (st || tokens == 0) return st;
+    const uint8_t* table = static_cast<const uint8_t*>(table_v);
+    const unsigned chunks = static_cast<unsigned>((dim / 4 + kChunk - 1) / kChunk);
+    const dim3 grid(grid_1d(tokens, 1, 1 << 20), chunks);
+    const bool bytes = !aligned(table, 2);
+    const bool vec_out = aligned(out, 16);
+    if (bytes) {
+        if (vec_out)
+            return launch(q8_gather_kernel<true, true>, grid, dim3(kChunk), 0, s, out, table, vocab, ids,
+                          single_id, tokens, dim);
+        return launch(q8_gather_kernel<true, false>, grid, dim3(kChunk), 0, s, out, table, vocab, ids,
+                      single_id, tokens, dim);
+    }
+    if (vec_out)
+        return launch(q8_gather_kernel<false, true>, grid, dim3(kChunk), 0, s, out, table, vocab, ids,
+                      single_id, tokens, dim);
+    return launch(q8_gather_kernel<false, false>, grid, dim3(kChunk), 0, s, out, table, vocab, ids,
+                  single_id, tokens, dim);
+}
+
+template <bool BYTES>
+int gather_rms_vec(float* out, const uint8_t* table, int64_t vocab, const int32_t* ids,
+                   int64_t tokens, int dim, const float* w, float eps, unsigned threads, int vpt,
+                   hipStream_t s) {
+    const unsigned grid = grid_1d(tokens, 1, 1 << 20);
+    if (vpt <= 2)
+        return launch(q8_gather_rms_kernel<BYTES, 2>, dim3(grid), dim3(threads), 0, s, out, table,
+                      vocab, ids, tokens, dim, w, eps, vpt);
+    return launch(q8_gather_rms_kernel<BYTES, 8>, dim3(grid), dim3(threads), 0, s, out, table, vocab,
+                  ids, tokens, dim, w, eps, vpt);
+}
+
+int gather_rms_launch(float* out, const void* table_v, int64_t vocab, const int32_t* ids,
+                      int64_t tokens, int dim, const float* w, float eps, hipStream_t s) {
+    const int st = check_common(out, table_v, tokens, dim, vocab, ids);
+    if (st) return st;
+    if (!w || !aligned(w, 4) || (!ids && tokens > 0)) return FENCE_ERROR_INVALID_VALUE;
     if (tokens == 0) return FENCE_SUCCESS;
-    const int rb = (dim / 32) * 34;
-    const bool vec = dim <= kMaxDimVec && aligned(out, 16) && (!NORM || aligned(w, 16));
+    const uint8_t* table = static_cast<const uint8_t*>(table_v);
+    unsigned threads = 0;
+    int vpt = 0;
+    const bool vec = dim <= kMaxDimVec && aligned(out, 16) && aligned(w, 16) &&
+                     pick_row_shape(dim / 4, 8, &threads, &vpt);
     if (vec) {
-        int stage = kStage1;
-        if (aligned(table, 16) && rb % 16 == 0) stage = kStage16;
-        else if (aligned(table, 2)) stage = kStage2;
-        const int dim4 = dim / 4;
-        const int vpt = (dim4 + kThreads - 1) / kThreads;
-        if (vpt <= 4) return vec_launch<NORM, 4>(out, table, vocab, ids, single_id, tokens, dim, w, eps, vpt, stage, s);
-        if (vpt <= 8) return vec_launch<NORM, 8>(out, table, vocab, ids, single_id, tokens, dim, w, eps, vpt, stage, s);
-        return vec_launch<NORM, 16>(out, table, vocab, ids, single_id, tokens, dim, w, eps, vpt, stage, s);
+        if (!aligned(table, 2))
+            return gather_rms_vec<true>(out, table, vocab, ids, tokens, dim, w, eps, threads, vpt, s);
+        return gather_rms_vec<false>(out, table, vocab, ids, tokens, dim, w, eps, threads, vpt, s);
     }
     const unsigned grid = grid_1d(tokens, 1, 1 << 20);
-    return launch(q8_gather_scalar_kernel<NORM>, dim3(grid), dim3(kThreads), 0, s, out, table, vocab,
-                  ids, single_id, tokens, dim, w, eps);
+    return launch(q8_gather_rms_scalar_kernel, dim3(grid), dim3(256), 0, s, out, table, vocab, ids,
+                  tokens, dim, w, eps);
 }
 
 }  // namespace
@@ -191,20 +227,18 @@ extern "C" int fence_embed_q8_0(float* out, const void* weight, int token_id, in
                                 hipStream_t stream) {
     if (token_id < 0) return FENCE_ERROR_INVALID_VALUE;
     // The reference signature carries no vocab size: the row is trusted.
-    return fence::gather_launch<false>(out, weight, INT64_MAX, nullptr, token_id, 1, dim, nullptr,
-                                       0.0f, stream);
+    return fence::gather_launch(out, weight, INT64_MAX, nullptr, token_id, 1, dim, stream);
 }
 
 extern "C" int fence_embed_q8_0_gather(float* out, const void* table, int64_t vocab,
                                        const int32_t* ids, int64_t tokens, int dim,
                                        hipStream_t stream) {
     if (!ids && tokens > 0) return FENCE_ERROR_INVALID_VALUE;
-    return fence::gather_launch<false>(out, table, vocab, ids, 0, tokens, dim, nullptr, 0.0f, stream);
+    return fence::gather_launch(out, table, vocab, ids, 0, tokens, dim, stream);
 }
 
 extern "C" int fence_embed_q8_0_gather_rms_norm(float* out, const void* table, int64_t vocab,
                                                 const int32_t* ids, int64_t tokens, int dim,
                                                 const float* w, float eps, hipStream_t stream) {
-    if (!ids && tokens > 0) return FENCE_ERROR_INVALID_VALUE;
-    return fence::gather_launch<true>(out, table, vocab, ids, 0, tokens, dim, w, eps, stream);
+    return fence::gather_rms_launch(out, table, vocab, ids, tokens, dim, w, eps, stream);
 }

@@ -8,7 +8,7 @@
 //   freq[p] = 1.0f / powf(base, (float)(2p)/(float)hd)    (ops.cuh:133),
 //   a = (float)pos * freq[p];  x0' = x0 cos a - x1 sin a;  x1' = x0 sin a + x1 cos a.
 //
-// Layout of the vector kernel: one workgroup per token.  A token's q and k
+// Layout of the vector kernel: one workgroup (up to 16 waves) per token.  A token's q and k
 // heads are cut into "units" of 8 floats, elements [4i, 4i+4) and
 // [hd/2 + 4i, hd/2 + 4i + 4) of one head (i < hd/8), so a lane holds four
 // whole NeoX pairs -- or four whole interleaved pairs -- and never needs a
@@ -34,20 +34,16 @@ struct InvFreq {
 
 namespace {
 
-constexpr int kMaxSlots = 8;
-
-template <int ROPE, int NORM, int G>
-__global__ __launch_bounds__(256) void head_ops_vec_kernel(
+template <int ROPE, int NORM, int G, int MAXS>
+__global__ __launch_bounds__(1024) void head_ops_vec_kernel(
     float* qo, const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
     int nkv, int slots, float eps, const int32_t* positions, int pos0, InvFreq tab) {
     constexpr int HD = 8 * G;
     constexpr int HALF = 4 * G;
     __shared__ __align__(16) float cs[2 * HALF];  // cos[HALF] then sin[HALF]
-    __shared__ float red[4];
+    __shared__ float red[16];
     const int T = blockDim.x;
     const int U = (nq + nkv) * G;
-    const float inv_row_n = 1.0f / static_cast<float>(nq * HD);
-    (void)inv_row_n;
 
     for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
         const int pos = positions ? positions[t] : pos0 + static_cast<int>(t);
@@ -55,9 +51,9 @@ __global__ __launch_bounds__(256) void head_ops_vec_kernel(
         float* qrow_out = qo + t * nq * HD;
         float* krow = k + t * nkv * HD;
 
-        f4 a[kMaxSlots], b[kMaxSlots];
+        f4 a[MAXS], b[MAXS];
 #pragma unroll
-        for (int s = 0; s < kMaxSlots; ++s) {
+        for (int s = 0; s < MAXS; ++s) {
             const int u = threadIdx.x + s * T;
             a[s] = f4(0.0f);
             b[s] = f4(0.0f);
@@ -65,8 +61,8 @@ __global__ __launch_bounds__(256) void head_ops_vec_kernel(
                 const int h = u / G;
                 const int i = u % G;
                 const float* src = (h < nq) ? qrow_in + h * HD : krow + (h - nq) * HD;
-                a[s] = ld4<false>(src + 4 * i);
-                b[s] = ld4<false>(src + HALF + 4 * i);
+                a[s] = ld4<true>(src + 4 * i);
+                b[s] = ld4<true>(src + HALF + 4 * i);
             }
         }
 
@@ -84,7 +80,7 @@ __global__ __launch_bounds__(256) void head_ops_vec_kernel(
         if constexpr (NORM == kNormRow) {
             float ss = 0.0f;
 #pragma unroll
-            for (int s = 0; s < kMaxSlots; ++s) {
+            for (int s = 0; s < MAXS; ++s) {
                 const int u = threadIdx.x + s * T;
                 if (s < slots && u < nq * G) ss += dot4(a[s]) + dot4(b[s]);
             }
@@ -92,10 +88,10 @@ __global__ __launch_bounds__(256) void head_ops_vec_kernel(
             rrow = rsqrtf(tot / static_cast<float>(nq * HD) + eps);
         }
 
-        float rh[kMaxSlots];
+        float rh[MAXS];
         if constexpr (NORM == kNormHead) {
 #pragma unroll
-            for (int s = 0; s < kMaxSlots; ++s) {
+            for (int s = 0; s < MAXS; ++s) {
                 float ss = 0.0f;
                 if (s < slots) ss = dot4(a[s]) + dot4(b[s]);
                 if (s < slots) {  // slots is uniform: whole waves enter together
@@ -110,7 +106,7 @@ __global__ __launch_bounds__(256) void head_ops_vec_kernel(
         if constexpr (ROPE != kRopeNone || NORM == kNormRow) __syncthreads();
 
 #pragma unroll
-        for (int s = 0; s < kMaxSlots; ++s) {
+        for (int s = 0; s < MAXS; ++s) {
             const int u = threadIdx.x + s * T;
             if (!(s < slots && u < U)) continue;
             const int h = u / G;
@@ -151,8 +147,8 @@ __global__ __launch_bounds__(256) void head_ops_vec_kernel(
                 vb.w = y.z * sb.y + y.w * cb.y;
             }
             float* dst = isq ? qrow_out + h * HD : krow + (h - nq) * HD;
-            st4<false>(dst + 4 * i, va);
-            st4<false>(dst + HALF + 4 * i, vb);
+            st4<true>(dst + 4 * i, va);
+            st4<true>(dst + HALF + 4 * i, vb);
         }
         __syncthreads();  // cs[] and red[] are rewritten for the next token
     }
@@ -221,20 +217,34 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(
     }
 }
 
+template <int ROPE, int NORM, int G>
+int dispatch_slots(unsigned grid, unsigned threads, hipStream_t s, float* qo, const float* qi,
+                   float* k, const float* wq, const float* wk, int64_t tokens, int nq, int nkv,
+                   int slots, float eps, const int32_t* positions, int pos0, const InvFreq& tab) {
+    if (slots <= 1)
+        return launch(head_ops_vec_kernel<ROPE, NORM, G, 1>, dim3(grid), dim3(threads), 0, s, qo, qi,
+                      k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+    if (slots <= 2)
+        return launch(head_ops_vec_kernel<ROPE, NORM, G, 2>, dim3(grid), dim3(threads), 0, s, qo, qi,
+                      k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+    return launch(head_ops_vec_kernel<ROPE, NORM, G, 4>, dim3(grid), dim3(threads), 0, s, qo, qi, k,
+                  wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+}
+
 template <int ROPE, int NORM>
 int dispatch_vec(int G, unsigned grid, unsigned threads, hipStream_t s, float* qo, const float* qi,
                  float* k, const float* wq, const float* wk, int64_t tokens, int nq, int nkv,
                  int slots, float eps, const int32_t* positions, int pos0, const InvFreq& tab) {
     switch (G) {
         case 8:
-            return launch(head_ops_vec_kernel<ROPE, NORM, 8>, dim3(grid), dim3(threads), 0, s, qo, qi,
-                          k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+            return dispatch_slots<ROPE, NORM, 8>(grid, threads, s, qo, qi, k, wq, wk, tokens, nq, nkv,
+                                                 slots, eps, positions, pos0, tab);
         case 16:
-            return launch(head_ops_vec_kernel<ROPE, NORM, 16>, dim3(grid), dim3(threads), 0, s, qo,
-                          qi, k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+            return dispatch_slots<ROPE, NORM, 16>(grid, threads, s, qo, qi, k, wq, wk, tokens, nq,
+                                                  nkv, slots, eps, positions, pos0, tab);
         case 32:
-            return launch(head_ops_vec_kernel<ROPE, NORM, 32>, dim3(grid), dim3(threads), 0, s, qo,
-                          qi, k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+            return dispatch_slots<ROPE, NORM, 32>(grid, threads, s, qo, qi, k, wq, wk, tokens, nq,
+                                                  nkv, slots, eps, positions, pos0, tab);
         default:
             return FENCE_ERROR_INVALID_VALUE;
     }
@@ -328,22 +338,7 @@ int head_ops_launch(float* qo, const float* qi, float* k, const float* wq, const
                ok16(wq) && ok16(wk);
     unsigned threads = 256;
     int slots = 0;
-    if (vec) {
-        const int64_t U = static_cast<int64_t>(nq + nkv) * G;
-        // smallest idle-lane count over workgroup sizes 64..256, preferring larger groups
-        int64_t best_idle = -1;
-        for (int th = 256; th >= 64; th -= 64) {
-            const int64_t sl = (U + th - 1) / th;
-            if (sl > kMaxSlots) continue;
-            const int64_t idle = sl * th - U;
-            if (best_idle < 0 || idle < best_idle) {
-                best_idle = idle;
-                threads = th;
-                slots = static_cast<int>(sl);
-            }
-        }
-        if (best_idle < 0) vec = false;
-    }
+    if (vec) vec = pick_row_shape(static_cast<int64_t>(nq + nkv) * G, 4, &threads, &slots);
     const unsigned grid = grid_1d(tokens, 1, 1 << 20);
     switch (rope) {
         case kRopeNone:

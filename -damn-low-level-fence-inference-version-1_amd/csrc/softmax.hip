@@ -5,9 +5,9 @@
 //   m = max(-1e30f, x_i);  e_i = expf(x_i - m);  x_i = e_i * (1.0f / sum e).
 // The reference makes five global passes over the row (read for max,
 // read+write exp, read+write scale).  Here a row is read once into VGPRs
-// with 128-bit loads (one wave per row up to 4096 floats, one 256-thread
-// workgroup per row up to 16384), max and sum are DPP/readlane reductions,
-// and the row is written once.
+// with 128-bit loads (one workgroup of up to 16 waves per row, one or two
+// float4 per lane where the row allows), max and sum are DPP/readlane
+// reductions with one LDS exchange across waves, and the row is written once.
 // Causal form: query i of sq sees keys 0 .. i + (sk - sq).  Keys past that
 // bound are not read (whole masked float4 chunks are skipped) and are
 // written as exactly 0.
@@ -28,33 +28,24 @@ __device__ __forceinline__ int row_valid(int64_t r, int n, int causal, int sq, i
     return v < 0 ? 0 : (v > n ? n : v);
 }
 
-// NWAVES waves cooperate on one row; a 256-thread workgroup holds
-// 4 / NWAVES rows.  MAXV float4 registers per lane, `vpt` of them used.
-template <int NWAVES, int MAXV>
-__global__ __launch_bounds__(256) void softmax_vec_kernel(float* x, int64_t rows, int n,
-                                                          int64_t ld, int causal, int sq, int shift,
-                                                          int vpt) {
-    constexpr int TPR = NWAVES * kWave;
-    constexpr int RPB = 256 / TPR;
-    __shared__ float red_max[4];
-    __shared__ float red_sum[4];
-    const int lt = threadIdx.x % TPR;
-    const int sub = threadIdx.x / TPR;
-    float* rm = red_max + sub * NWAVES;
-    float* rsum = red_sum + sub * NWAVES;
-
-    for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * RPB; r0 < rows;
-         r0 += static_cast<int64_t>(gridDim.x) * RPB) {
-        const int64_t r = r0 + sub;
-        const bool live = r < rows;  // uniform per wave
-        float* row = x + (live ? r : 0) * ld;
-        const int valid = live ? row_valid(r, n, causal, sq, shift) : 0;
+// One workgroup per row, up to 16 waves, MAXV float4 registers per lane
+// (`vpt` of them used).
+template <int MAXV>
+__global__ __launch_bounds__(1024) void softmax_vec_kernel(float* x, int64_t rows, int n,
+                                                           int64_t ld, int causal, int sq, int shift,
+                                                           int vpt) {
+    __shared__ float red_max[16];
+    __shared__ float red_sum[16];
+    const int T = blockDim.x;
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        float* row = x + r * ld;
+        const int valid = row_valid(r, n, causal, sq, shift);
 
         f4 v[MAXV];
         float m = -1e30f;
 #pragma unroll
         for (int j = 0; j < MAXV; ++j) {
-            const int e0 = 4 * (lt + j * TPR);
+            const int e0 = 4 * (static_cast<int>(threadIdx.x) + j * T);
             v[j] = f4(kNegInf);
             if (j < vpt && e0 < valid) {
                 if (e0 + 4 <= valid) {
@@ -67,14 +58,13 @@ __global__ __launch_bounds__(256) void softmax_vec_kernel(float* x, int64_t rows
                 m = fmaxf(m, max4(v[j]));
             }
         }
-        if constexpr (NWAVES == 1) m = wave_reduce(m, OpMax());
-        else m = block_reduce<NWAVES>(m, OpMax(), rm);
+        m = block_reduce_dyn(m, OpMax(), red_max);
 
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < MAXV; ++j) {
             // whole chunk j of this row beyond the causal bound: nothing to do
-            if (j < vpt && 4 * j * TPR < valid) {
+            if (j < vpt && 4 * j * T < valid) {
                 v[j].x = expf(v[j].x - m);
                 v[j].y = expf(v[j].y - m);
                 v[j].z = expf(v[j].z - m);
@@ -82,31 +72,28 @@ __global__ __launch_bounds__(256) void softmax_vec_kernel(float* x, int64_t rows
                 s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
             }
         }
-        if constexpr (NWAVES == 1) s = wave_reduce(s, OpAdd());
-        else s = block_reduce<NWAVES>(s, OpAdd(), rsum);
+        s = block_reduce_dyn(s, OpAdd(), red_sum);
         const float inv = 1.0f / s;
 
-        if (live) {
 #pragma unroll
-            for (int j = 0; j < MAXV; ++j) {
-                const int e0 = 4 * (lt + j * TPR);
-                if (j < vpt && e0 < n) {
-                    f4 o;
-                    o.x = (e0 + 0 < valid) ? v[j].x * inv : 0.0f;
-                    o.y = (e0 + 1 < valid) ? v[j].y * inv : 0.0f;
-                    o.z = (e0 + 2 < valid) ? v[j].z * inv : 0.0f;
-                    o.w = (e0 + 3 < valid) ? v[j].w * inv : 0.0f;
-                    if (e0 + 4 <= n) {
-                        st4<true>(row + e0, o);
-                    } else {
-                        row[e0] = o.x;
-                        if (e0 + 1 < n) row[e0 + 1] = o.y;
-                        if (e0 + 2 < n) row[e0 + 2] = o.z;
-                    }
+        for (int j = 0; j < MAXV; ++j) {
+            const int e0 = 4 * (static_cast<int>(threadIdx.x) + j * T);
+            if (j < vpt && e0 < n) {
+                f4 o;
+                o.x = (e0 + 0 < valid) ? v[j].x * inv : 0.0f;
+                o.y = (e0 + 1 < valid) ? v[j].y * inv : 0.0f;
+                o.z = (e0 + 2 < valid) ? v[j].z * inv : 0.0f;
+                o.w = (e0 + 3 < valid) ? v[j].w * inv : 0.0f;
+                if (e0 + 4 <= n) {
+                    st4<true>(row + e0, o);
+                } else {
+                    row[e0] = o.x;
+                    if (e0 + 1 < n) row[e0 + 1] = o.y;
+                    if (e0 + 2 < n) row[e0 + 2] = o.z;
                 }
             }
         }
-        if constexpr (NWAVES > 1) __syncthreads();
+        __syncthreads();  // red_max / red_sum are rewritten by the next row
     }
 }
 
@@ -131,27 +118,21 @@ __global__ __launch_bounds__(256) void softmax_scalar_kernel(float* x, int64_t r
     }
 }
 
-template <int NWAVES, int MAXV>
-int vec_launch(float* x, int64_t rows, int n, int64_t ld, int causal, int sq, int shift, int vpt,
-               hipStream_t s) {
-    constexpr int RPB = 4 / NWAVES;
-    const unsigned grid = grid_1d(rows, RPB, 1 << 20);
-    return launch(softmax_vec_kernel<NWAVES, MAXV>, dim3(grid), dim3(256), 0, s, x, rows, n, ld,
-                  causal, sq, shift, vpt);
-}
-
 int softmax_launch(float* x, int64_t rows, int n, int64_t ld, int causal, int sq, int shift,
                    hipStream_t s) {
-    const bool vec = aligned(x, 16) && (ld % 4 == 0);
-    const int n4 = (n + 3) / 4;
-    if (vec) {
-        if (n4 <= kWave * 4) return vec_launch<1, 4>(x, rows, n, ld, causal, sq, shift, (n4 + 63) / 64, s);
-        if (n4 <= kWave * 8) return vec_launch<1, 8>(x, rows, n, ld, causal, sq, shift, (n4 + 63) / 64, s);
-        if (n4 <= kWave * 16) return vec_launch<1, 16>(x, rows, n, ld, causal, sq, shift, (n4 + 63) / 64, s);
-        if (n4 <= 256 * 16) return vec_launch<4, 16>(x, rows, n, ld, causal, sq, shift, (n4 + 255) / 256, s);
-    }
     const unsigned grid = grid_1d(rows, 1, 1 << 20);
-    return launch(softmax_scalar_kernel, dim3(grid), dim3(256), 0, s, x, rows, n, ld, causal, sq, shift);
+    const bool vec = aligned(x, 16) && (ld % 4 == 0);
+    unsigned threads = 0;
+    int vpt = 0;
+    if (vec && pick_row_shape((n + 3) / 4, 16, &threads, &vpt)) {
+        if (vpt <= 2)
+            return launch(softmax_vec_kernel<2>, dim3(grid), dim3(threads), 0, s, x, rows, n, ld,
+                          causal, sq, shift, vpt);
+        return launch(softmax_vec_kernel<16>, dim3(grid), dim3(threads), 0, s, x, rows, n, ld,
+                      causal, sq, shift, vpt);
+    }
+    return launch(softmax_scalar_kernel, dim3(grid), dim3(256), 0, s, x, rows, n, ld, causal, sq,
+                  shift);
 }
 
 }  // namespace

@@ -10,3 +10,8 @@ extern "C" const char* fence_status_string(int status) {
 }
 
 extern "C" const char* fence_version(void) { return "fence-mi355x 0.1.0 (gfx950)"; }
+
+extern "C" int fence_time_next_launch(hipEvent_t start, hipEvent_t stop) {
+    fence::timing_hook() = fence::TimingHook{start, stop};
+    return FENCE_SUCCESS;
+}

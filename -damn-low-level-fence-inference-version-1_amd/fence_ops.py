@@ -47,6 +47,7 @@ SIGNATURES = {
     "fence_embed_q8_0_gather": (_P, _P, _L, _P, _L, _I, _P),
     "fence_embed_q8_0_gather_rms_norm": (_P, _P, _L, _P, _L, _I, _P, _F, _P),
     "fence_rope_inv_freq": (_P, _I, _F),
+    "fence_time_next_launch": (_P, _P),
     "fence_status_string": (_I,),
     "fence_version": (),
 }
@@ -163,6 +164,12 @@ def embed_q8_0_gather(out, table, vocab, ids, tokens, dim, stream=None):
 
 def embed_q8_0_gather_rms_norm(out, table, vocab, ids, tokens, dim, w, eps, stream=None):
     _call("fence_embed_q8_0_gather_rms_norm", out, table, vocab, ids, tokens, dim, w, eps, stream)
+
+
+def time_next_launch(start, stop) -> None:
+    """Record hipEvent handles `start`/`stop` around the next kernel this
+    thread launches (kernel execution interval only)."""
+    _call("fence_time_next_launch", start, stop)
 
 
 def rope_inv_freq(head_dim: int, freq_base: float):

@@ -13,8 +13,11 @@ once) / time, as GB/s, with inputs resident in HBM.  Cold protocol: the step
 rotates over buffer sets totalling more than 1 GiB, so no step finds its data
 in the 256 MB Infinity Cache or the L2s.
 
-Also reported: per-op time and GB/s measured with HIP events on the launch
-stream inside the timed region, the roofline of the dominant kernel (swiglu),
+Also reported: per-op kernel time and GB/s measured inside the timed region
+with HIP events that the launch itself records at the kernel's dispatch
+start and end (fence_time_next_launch -> hipExtLaunchKernel, on the launch
+stream: the interval a kernel-trace profiler reports), the roofline of the
+dominant kernel (swiglu),
 the Llama-3-8B decode-step op set in microseconds, a device-copy
 calibration, and the CPU baseline (the scalar oracle on one host core,
 timed on a bounded sample of the same step).
@@ -55,7 +58,7 @@ BYTES = {
 }
 STEP_BYTES = sum(BYTES.values())
 DOMINANT = "swiglu"
-KERNEL_NAMES = {"gather": "q8_gather_vec_kernel", "norm_rope": "head_ops_vec_kernel",
+KERNEL_NAMES = {"gather": "q8_gather_kernel", "norm_rope": "head_ops_vec_kernel",
                 "swiglu": "swiglu_vec_kernel"}
 
 
@@ -94,6 +97,40 @@ class BufferSet:
         self.gate = torch.randn(T, FFN, **f)
         self.up = torch.randn(T, FFN, **f)
         self.act = torch.empty(T, FFN, device="cuda")
+
+
+class HipEvents:
+    """Raw hipEvent handles from the HIP runtime already loaded in-process."""
+
+    def __init__(self):
+        import ctypes
+        self.c = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.made = []
+
+    def create(self):
+        ev = self.c.c_void_p()
+        rc = self.hip.hipEventCreate(self.c.byref(ev))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed: {rc}")
+        self.made.append(ev.value)
+        return ev.value
+
+    def elapsed_ms(self, a, b):
+        ms = self.c.c_float()
+        rc = self.hip.hipEventElapsedTime(self.c.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return ms.value
+
+    def destroy_all(self):
+        for e in self.made:
+            self.hip.hipEventDestroy(e)
+        self.made = []
 
 
 def read_traffic(kernel_key: str):
@@ -176,8 +213,11 @@ def main():
         for op in ops:
             launch(op, sets[i % nsets])
 
-    ev = {op: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(args.steps)] for op in ops}
+    # Timed region: K steps.  The dominant kernel records its own start/end
+    # (hipExtLaunchKernel events) every step; the other two launch plainly,
+    # so the host's launch rate stays ahead of the GPU.
+    hev = HipEvents()
+    dom_ev = [(hev.create(), hev.create()) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
@@ -186,21 +226,19 @@ def main():
     for i in range(args.steps):
         b = sets[i % nsets]
         for op in ops:
-            e0, e1 = ev[op][i]
-            e0.record(stream)
+            if op == DOMINANT:
+                F.time_next_launch(*dom_ev[i])
             launch(op, b)
-            e1.record(stream)
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_total = t_start.elapsed_time(t_end)
     ms_per_step = ms_total / args.steps
 
-    per_op = {}
-    for op in ops:
-        ts = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev[op])  # us
+    def summarize(op, ts_us):
+        ts = sorted(ts_us)
         mean = sum(ts) / len(ts)
-        per_op[op] = {
+        return {
             "us_mean": round(mean, 3),
             "us_p10": round(ts[len(ts) // 10], 3),
             "us_p50": round(ts[len(ts) // 2], 3),
@@ -211,12 +249,27 @@ def main():
             "kernel": KERNEL_NAMES[op],
         }
 
+    dom = summarize(DOMINANT, [hev.elapsed_ms(a, b) * 1e3 for a, b in dom_ev])
+
+    # Per-op pass: every launch of every op timed the same way, same cold
+    # rotation, ops launched one kind at a time.
+    per_op = {}
+    reps = max(20, min(args.steps, 200))
+    for op in ops:
+        evs = [(hev.create(), hev.create()) for _ in range(reps)]
+        for i in range(reps):
+            F.time_next_launch(*evs[i])
+            launch(op, sets[(i + 3) % nsets])
+        torch.cuda.synchronize()
+        per_op[op] = summarize(op, [hev.elapsed_ms(a, b) * 1e3 for a, b in evs])
+    hev.destroy_all()
+
     value = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
-    dom = per_op[DOMINANT]
     traffic = read_traffic(DOMINANT)
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                 "frac": dom["frac_peak"], "traffic": traffic, "kernel": KERNEL_NAMES[DOMINANT],
-                "algorithmic_bytes_per_launch": BYTES[DOMINANT]}
+                "algorithmic_bytes_per_launch": BYTES[DOMINANT], "us_mean": dom["us_mean"],
+                "us_p50": dom["us_p50"], "launches_timed": args.steps}
 
     decode = decode_op_set(torch, F, gen, args.decode_reps)
     copy_gbps = copy_calibration(torch)
@@ -272,6 +325,7 @@ def decode_op_set(torch, F, gen, reps):
     scores = torch.randn(NQ, max_ctx, device="cuda", generator=gen) * (3 / 128 ** 0.5)
     gate = torch.randn(FFN, device="cuda", generator=gen)
     up = torch.randn(FFN, device="cuda", generator=gen)
+    act = torch.empty(FFN, device="cuda")
     s = torch.cuda.current_stream()
     sh = s.cuda_stream
     tok = 9707
@@ -282,7 +336,7 @@ def decode_op_set(torch, F, gen, reps):
         F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, THETA, F.ROPE_INTERLEAVED, sh)
         F.softmax_rows(scores.data_ptr(), NQ, pos + 1, max_ctx, sh)
         F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), HIDDEN, 1e-5, sh)
-        F.silu_elementwise_mul(gate.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh)
+        F.silu_elementwise_mul(act.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh)
 
     for _ in range(20):
         step()
@@ -315,7 +369,7 @@ def decode_op_set(torch, F, gen, reps):
             F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, THETA, F.ROPE_INTERLEAVED, sh_cap)
             F.softmax_rows(scores.data_ptr(), NQ, pos + 1, max_ctx, sh_cap)
             F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), HIDDEN, 1e-5, sh_cap)
-            F.silu_elementwise_mul(gate.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh_cap)
+            F.silu_elementwise_mul(act.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh_cap)
         for _ in range(10):
             g.replay()
         torch.cuda.synchronize()

@@ -13,7 +13,8 @@
  *     (checked on the host before anything is launched), or
  *     FENCE_ERROR_HIP_BASE + hipError_t when the launch itself fails;
  *   - never allocates, never synchronises, never exits; no global mutable
- *     state, so calls are re-entrant from any host thread;
+ *     state (only per-thread caches), so calls are re-entrant from any host
+ *     thread;
  *   - 16-byte aligned rows take the 128-bit vector kernels; other alignments
  *     take scalar kernels with the same results (not an error);
  *   - in-place forms the reference's callers rely on keep working:
@@ -171,6 +172,15 @@ int fence_embed_q8_0_gather_rms_norm(float* out, const void* table,
  * p < head_dim/2 (src/kernels/ops.cuh:133), computed on the host: the RoPE
  * kernels receive exactly these values. */
 int fence_rope_inv_freq(float* inv_freq, int head_dim, float freq_base);
+
+/* Kernel timing: the next kernel this host thread launches through this
+ * library records `start` and `stop` (events from hipEventCreate) at its own
+ * dispatch start and end (hipExtLaunchKernel), so hipEventElapsedTime gives
+ * the kernel's execution time without queueing or dispatch latency -- the
+ * interval a kernel-trace profiler reports.  One-shot; NULL, NULL cancels.
+ * No counterpart in the reference (it has no timing facility); used by the
+ * benchmark. */
+int fence_time_next_launch(hipEvent_t start, hipEvent_t stop);
 
 /* Static text for a status code. */
 const char* fence_status_string(int status);

@@ -16,6 +16,13 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
+@pytest.fixture(autouse=True)
+def _release_device_inputs():
+    yield
+    import gpu_util
+    gpu_util.LIVE.clear()
+
+
 @pytest.fixture(scope="session")
 def oracle():
     from oracle_py import Oracle

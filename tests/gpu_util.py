@@ -15,9 +15,17 @@ def torch_mod():
     return torch
 
 
+# Every tensor dev() makes stays referenced until the test ends (conftest
+# clears the list), so `dev(x).data_ptr()` written inline in a call cannot be
+# freed -- and its memory handed to the next dev() -- before the kernel runs.
+LIVE: list = []
+
+
 def dev(a: np.ndarray):
     torch = torch_mod()
-    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    LIVE.append(t)
+    return t
 
 
 def host(t) -> np.ndarray:
