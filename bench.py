@@ -71,6 +71,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--decode-reps", type=int, default=300)
+    ap.add_argument("--all", metavar="PATH", default=None,
+                    help="also measure every op of BASELINE.json configs[0..4] and write the "
+                         "per-op report (JSON) to PATH; a table goes to stderr")
+    ap.add_argument("--all-reps", type=int, default=50)
     return ap.parse_args()
 
 
@@ -275,6 +279,10 @@ def main():
     copy_gbps = copy_calibration(torch)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    if args.all:
+        del sets
+        torch.cuda.empty_cache()
+        all_configs(torch, F, args.all, args.all_reps)
 
     line = {
         "metric": METRIC,
@@ -386,6 +394,165 @@ def decode_op_set(torch, F, gen, reps):
     except Exception as exc:  # graph capture is optional for the report
         out["graph_error"] = str(exc)[:200]
     return out
+
+
+def all_configs(torch, F, path, reps):
+    """Every op of BASELINE.json configs[0..4] on seeded synthetic inputs.
+    Each launch records its own kernel start/end; inputs rotate over enough
+    buffer sets (>= 1 GiB in total, at least 2) that no launch finds its data
+    in the Infinity Cache or the L2s.  Bytes are algorithmic (inputs read
+    once, outputs written once)."""
+    gen = torch.Generator(device="cuda").manual_seed(99)
+    dev = dict(device="cuda")
+    hev = HipEvents()
+    sh = torch.cuda.current_stream().cuda_stream
+    results = []
+
+    def nsets_for(set_bytes):
+        return max(2, -(-(1 << 30) // max(set_bytes, 1)) + 1)
+
+    scrub = {"buf": None}
+
+    def measure(cfg, name, nbytes, make_set, run, note=""):
+        probe = make_set()
+        sb = sum(t.numel() * t.element_size() for t in probe.values() if torch.is_tensor(t))
+        small = sb < (16 << 20)
+        sets = [probe] + [make_set() for _ in range(1 if small else nsets_for(sb) - 1)]
+        if small and scrub["buf"] is None:
+            scrub["buf"] = torch.empty((1 << 30) // 4, **dev)
+        for i in range(3):
+            run(sets[i % len(sets)])
+        evs = [(hev.create(), hev.create()) for _ in range(reps)]
+        for i in range(reps):
+            if small:  # untimed 1 GiB write evicts the small inputs from every cache level
+                scrub["buf"].zero_()
+            F.time_next_launch(*evs[i])
+            run(sets[i % len(sets)])
+        torch.cuda.synchronize()
+        ts = sorted(hev.elapsed_ms(a, b) * 1e3 for a, b in evs)
+        mean = sum(ts) / len(ts)
+        gbps = nbytes / (mean * 1e-6) / 1e9
+        r = {"config": cfg, "op": name, "bytes": int(nbytes), "us_mean": round(mean, 3),
+             "us_p10": round(ts[len(ts) // 10], 3), "us_p50": round(ts[len(ts) // 2], 3),
+             "us_p90": round(ts[(9 * len(ts)) // 10], 3), "GBps": round(gbps, 1),
+             "frac_peak": round(gbps / PEAK_HBM_GBPS, 4), "sets": len(sets),
+             "cold": "1 GiB scrub between launches" if small else "rotating buffer sets"}
+        if note:
+            r["note"] = note
+        results.append(r)
+        print(f"[all] cfg{cfg} {name:34s} {mean:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / PEAK_HBM_GBPS:5.1f}%"
+              f"  ({nbytes / 1e6:.2f} MB, {len(sets)} sets)", file=sys.stderr, flush=True)
+        del sets
+        torch.cuda.empty_cache()
+
+    def randn(*shape):
+        return torch.randn(*shape, **dev, generator=gen)
+
+    # ---- configs[0]: Qwen3-4B decode, one token, fp32
+    E0, F0, V0 = 2560, 9728, 151936
+    pos0 = int(torch.randint(0, 4096, (1,), generator=torch.Generator().manual_seed(0)).item())
+    measure(0, "rms_norm 2560", 3 * E0 * 4,
+            lambda: dict(x=randn(E0), w=1 + 0.1 * randn(E0), o=torch.empty(E0, **dev)),
+            lambda b: F.rms_norm(b["o"].data_ptr(), b["x"].data_ptr(), b["w"].data_ptr(), E0, 1e-6, sh))
+    measure(0, "qk_norm_rope neox 32+8x128", 2 * 40 * 128 * 4 + 2 * 128 * 4,
+            lambda: dict(q=randn(32 * 128), k=randn(8 * 128), wq=1 + 0.1 * randn(128), wk=1 + 0.1 * randn(128)),
+            lambda b: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), b["wq"].data_ptr(), b["wk"].data_ptr(),
+                                     1, 32, 8, 128, 1e-6, None, pos0, 1e6, F.ROPE_NEOX, sh))
+    measure(0, "swiglu 9728", 3 * F0 * 4,
+            lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), F0, sh))
+    tab0 = [make_q8_0_table(torch, gen, V0, E0) for _ in range(2)]
+    tok0 = int(torch.randint(0, V0, (1,), generator=torch.Generator().manual_seed(1)).item())
+    flip = {"i": 0}
+
+    def embed0(b):
+        flip["i"] ^= 1
+        F.embed_q8_0(b["o"].data_ptr(), tab0[flip["i"]].data_ptr(), tok0, E0, sh)
+    measure(0, "embed_q8_0 1 id x 2560", E0 * 4 + E0 // 32 * 34 + 4,
+            lambda: dict(o=torch.empty(E0, **dev)), embed0)
+    del tab0
+
+    # ---- configs[1]: Llama-3-8B prefill T=512 (the bench step's ops)
+    T1, H1, F1, V1 = 512, 4096, 14336, 128256
+    w1 = 1 + 0.1 * randn(H1)
+    measure(1, "rms_norm->rope interleaved Q+K", BYTES["norm_rope"],
+            lambda: dict(x=randn(T1, H1), o=torch.empty(T1, H1, **dev), k=randn(T1, 8 * 128)),
+            lambda b: F.rms_norm_rope(b["o"].data_ptr(), b["x"].data_ptr(), w1.data_ptr(), b["k"].data_ptr(),
+                                      T1, 32, 8, 128, 1e-5, None, 0, 5e5, F.ROPE_INTERLEAVED, sh))
+    measure(1, "swiglu 512x14336", BYTES["swiglu"],
+            lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh))
+    tab1 = make_q8_0_table(torch, gen, V1, H1)
+    measure(1, "q8_0 gather 512 x 4096", BYTES["gather"],
+            lambda: dict(ids=torch.randint(0, V1, (T1,), dtype=torch.int32, **dev, generator=gen),
+                         o=torch.empty(T1, H1, **dev)),
+            lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), T1, H1, sh))
+    del tab1
+
+    # ---- configs[2]: Qwen3-8B long prefill T=4096
+    T2, F2 = 4096, 12288
+    wq2, wk2 = 1 + 0.1 * randn(128), 1 + 0.1 * randn(128)
+    for style, sname in ((F.ROPE_NEOX, "neox"), (F.ROPE_INTERLEAVED, "interleaved")):
+        measure(2, f"qk_norm_rope {sname} 4096x(32+8)x128", 2 * T2 * 40 * 128 * 4 + 2 * 128 * 4,
+                lambda: dict(q=randn(T2, 32 * 128), k=randn(T2, 8 * 128)),
+                lambda b, style=style: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), wq2.data_ptr(),
+                                                      wk2.data_ptr(), T2, 32, 8, 128, 1e-6, None, 0, 1e6,
+                                                      style, sh))
+    measure(2, "swiglu 4096x12288", 3 * T2 * F2 * 4,
+            lambda: dict(g=randn(T2, F2), u=randn(T2, F2), o=torch.empty(T2, F2, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T2 * F2, sh))
+
+    # ---- configs[3]: Qwen3-14B embedding batch, gather -> rms_norm, Zipf ids
+    T3, E3, V3 = 8192, 5120, 151936
+    w3 = 1 + 0.1 * randn(E3)
+    tabs3 = [make_q8_0_table(torch, gen, V3, E3) for _ in range(2)]
+    zw = torch.arange(1, V3 + 1, dtype=torch.float64) ** -1.1
+    zcdf = torch.cumsum(zw, 0)
+    zcdf /= zcdf[-1].clone()
+    zg = torch.Generator().manual_seed(3)
+
+    def zipf_ids():
+        u = torch.rand(T3, generator=zg, dtype=torch.float64)
+        return torch.clamp(torch.searchsorted(zcdf, u), max=V3 - 1).to(torch.int32).cuda()
+    ids3 = zipf_ids()
+    uniq = int(torch.unique(ids3).numel())
+    flip3 = {"i": 0}
+
+    def gather3(b):
+        flip3["i"] ^= 1
+        F.embed_q8_0_gather_rms_norm(b["o"].data_ptr(), tabs3[flip3["i"]].data_ptr(), V3, b["ids"].data_ptr(),
+                                     T3, E3, w3.data_ptr(), 1e-6, sh)
+    measure(3, "gather->rms_norm 8192 Zipf x 5120", T3 * E3 * 4 + uniq * (E3 // 32 * 34) + T3 * 4 + E3 * 4,
+            lambda: dict(ids=ids3, o=torch.empty(T3, E3, **dev)), gather3,
+            note=f"{uniq} unique rows; per-token-read bytes {T3 * E3 * 4 + T3 * (E3 // 32 * 34) + T3 * 4 + E3 * 4}")
+    del tabs3
+
+    # ---- configs[4]: Mixtral-8x7B elementwise stage
+    H4, S4 = 32, 2048
+
+    def scores():
+        sc = randn(H4, S4, S4) * (3.0 / 128 ** 0.5)
+        return sc.masked_fill_(torch.ones(S4, S4, dtype=torch.bool, **dev).triu_(1), float("-inf"))
+    measure(4, "causal softmax 32x2048x2048 (skip)", 805437440,
+            lambda: dict(s=scores()),
+            lambda b: F.softmax_causal(b["s"].data_ptr(), H4, S4, S4, sh),
+            note="causal-skip bytes: masked keys not read, all keys written; generic bytes 1073741824")
+    measure(4, "softmax rows 65536x2048 (generic)", 1073741824,
+            lambda: dict(s=scores()),
+            lambda b: F.softmax_rows(b["s"].data_ptr(), H4 * S4, S4, S4, sh))
+    T4, F4 = 8192, 14336
+    measure(4, "swiglu 8192x14336", 3 * T4 * F4 * 4,
+            lambda: dict(g=randn(T4, F4), u=randn(T4, F4), o=torch.empty(T4, F4, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T4 * F4, sh))
+    measure(4, "rope interleaved Q+K 8192x(32+8)x128", 2 * T4 * 40 * 128 * 4,
+            lambda: dict(q=randn(T4, 32 * 128), k=randn(T4, 8 * 128)),
+            lambda b: F.rope(b["q"].data_ptr(), b["k"].data_ptr(), T4, 32, 8, 128, None, 0, 1e6,
+                             F.ROPE_INTERLEAVED, sh))
+    hev.destroy_all()
+    scrub["buf"] = None
+    with open(path, "w") as fh:
+        json.dump({"peak_GBps": PEAK_HBM_GBPS, "reps": reps, "timing": "kernel start/end events (hipExtLaunchKernel)",
+                   "results": results}, fh, indent=1)
 
 
 def copy_calibration(torch):
