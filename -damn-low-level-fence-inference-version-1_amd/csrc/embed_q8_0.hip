@@ -18,35 +18,54 @@
 // rms_norm (src/kernels/ops.cuh:40-44) before the single write.
 #include "common.hpp"
 
+#ifndef FENCE_GATHER_RMS_VPT
+#define FENCE_GATHER_RMS_VPT 2
+#endif
+
 namespace fence {
 namespace {
 
 constexpr int kChunk = 256;        // float4 outputs per workgroup in the plain gather
-constexpr int kMaxDimVec = 32768;  // fused form: up to 8 float4 per lane at 1024 lanes
+constexpr int kMaxDimVec = 16384;  // fused form: up to 4 float4 per lane at 1024 lanes
 
-// One float4 of a dequantised row.  BYTES: table only 1-byte aligned.
+// The raw bits behind one float4 of a dequantised row: the block's fp16
+// scale and the four int8 of quarter f%8.  BYTES: table only 1-byte aligned.
+struct Q8Bits {
+    uint32_t d;
+    uint32_t q;
+};
+
 template <bool BYTES>
-__device__ __forceinline__ f4 dequant4(const uint8_t* row, int f) {
+__device__ __forceinline__ Q8Bits load_q8(const uint8_t* row, int f) {
     const uint8_t* blk = row + 34 * (f >> 3);
     const int k = f & 7;
-    uint32_t dbits, q;
+    Q8Bits r;
     if constexpr (BYTES) {
         const uint8_t* p = blk + 2 + 4 * k;
-        dbits = static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8);
-        q = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) |
-            (static_cast<uint32_t>(p[2]) << 16) | (static_cast<uint32_t>(p[3]) << 24);
+        r.d = static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8);
+        r.q = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8) |
+              (static_cast<uint32_t>(p[2]) << 16) | (static_cast<uint32_t>(p[3]) << 24);
     } else {
         const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
-        dbits = h[0];
-        q = static_cast<uint32_t>(h[1 + 2 * k]) | (static_cast<uint32_t>(h[2 + 2 * k]) << 16);
+        r.d = h[0];
+        r.q = static_cast<uint32_t>(h[1 + 2 * k]) | (static_cast<uint32_t>(h[2 + 2 * k]) << 16);
     }
-    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(dbits)));
+    return r;
+}
+
+__device__ __forceinline__ f4 dequant_bits(Q8Bits b) {
+    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b.d)));
     f4 v;
-    v.x = d * static_cast<float>(static_cast<int8_t>(q & 0xFFu));
-    v.y = d * static_cast<float>(static_cast<int8_t>((q >> 8) & 0xFFu));
-    v.z = d * static_cast<float>(static_cast<int8_t>((q >> 16) & 0xFFu));
-    v.w = d * static_cast<float>(static_cast<int8_t>(q >> 24));
+    v.x = d * static_cast<float>(static_cast<int8_t>(b.q & 0xFFu));
+    v.y = d * static_cast<float>(static_cast<int8_t>((b.q >> 8) & 0xFFu));
+    v.z = d * static_cast<float>(static_cast<int8_t>((b.q >> 16) & 0xFFu));
+    v.w = d * static_cast<float>(static_cast<int8_t>(b.q >> 24));
     return v;
+}
+
+template <bool BYTES>
+__device__ __forceinline__ f4 dequant4(const uint8_t* row, int f) {
+    return dequant_bits(load_q8<BYTES>(row, f));
 }
 
 template <bool VEC_OUT>
@@ -98,15 +117,24 @@ __global__ __launch_bounds__(1024) void q8_gather_rms_kernel(float* out, const u
         float* orow = out + t * dim;
         const bool ok = id >= 0 && id < vocab;  // uniform across the workgroup
         const uint8_t* row = table + (ok ? id : 0) * rb;
+        Q8Bits bits[MAXV];
+        f4 wv[MAXV];
+#pragma unroll
+        for (int j = 0; j < MAXV; ++j) {  // every load of the lane first, weights included
+            const int f = threadIdx.x + j * T;
+            bits[j] = Q8Bits{0u, 0u};
+            wv[j] = f4(0.0f);
+            if (j < vpt && f < dim4) {
+                wv[j] = ld4<false>(w + 4 * f);
+                if (ok) bits[j] = load_q8<BYTES>(row, f);
+            }
+        }
         f4 v[MAXV];
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < MAXV; ++j) {
-            const int f = threadIdx.x + j * T;
-            if (ok && j < vpt && f < dim4) {
-                v[j] = dequant4<BYTES>(row, f);
-                ss += dot4(v[j]);
-            }
+            v[j] = dequant_bits(bits[j]);  // zero bits give +0
+            ss += dot4(v[j]);
         }
         const float tot = block_reduce_dyn(ss, OpAdd(), red);
         const float rs = rsqrtf(tot / static_cast<float>(dim) + eps);
@@ -114,7 +142,7 @@ __global__ __launch_bounds__(1024) void q8_gather_rms_kernel(float* out, const u
         for (int j = 0; j < MAXV; ++j) {
             const int f = threadIdx.x + j * T;
             if (j < vpt && f < dim4) {
-                const f4 o = ok ? (ld4<false>(w + 4 * f) * v[j]) * rs : f4(__builtin_nanf(""));
+                const f4 o = ok ? (wv[j] * v[j]) * rs : f4(__builtin_nanf(""));
                 st4<true>(orow + 4 * f, o);
             }
         }
@@ -195,7 +223,7 @@ int gather_rms_vec(float* out, const uint8_t* table, int64_t vocab, const int32_
     if (vpt <= 2)
         return launch(q8_gather_rms_kernel<BYTES, 2>, dim3(grid), dim3(threads), 0, s, out, table,
                       vocab, ids, tokens, dim, w, eps, vpt);
-    return launch(q8_gather_rms_kernel<BYTES, 8>, dim3(grid), dim3(threads), 0, s, out, table, vocab,
+    return launch(q8_gather_rms_kernel<BYTES, 4>, dim3(grid), dim3(threads), 0, s, out, table, vocab,
                   ids, tokens, dim, w, eps, vpt);
 }
 
@@ -209,7 +237,7 @@ int gather_rms_launch(float* out, const void* table_v, int64_t vocab, const int3
     unsigned threads = 0;
     int vpt = 0;
     const bool vec = dim <= kMaxDimVec && aligned(out, 16) && aligned(w, 16) &&
-                     pick_row_shape(dim / 4, 8, &threads, &vpt);
+                     plan_row(tokens, dim / 4, FENCE_GATHER_RMS_VPT, 4, &threads, &vpt);
     if (vec) {
         if (!aligned(table, 2))
             return gather_rms_vec<true>(out, table, vocab, ids, tokens, dim, w, eps, threads, vpt, s);

@@ -21,6 +21,10 @@
 
 #include <cmath>
 
+#ifndef FENCE_HEAD_SLOTS
+#define FENCE_HEAD_SLOTS 2
+#endif
+
 namespace fence {
 
 enum { kRopeNone = -1, kRopeNeox = FENCE_ROPE_NEOX, kRopeInter = FENCE_ROPE_INTERLEAVED };
@@ -51,18 +55,30 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
         float* qrow_out = qo + t * nq * HD;
         float* krow = k + t * nkv * HD;
 
-        f4 a[MAXS], b[MAXS];
+        // every load of the lane first: its q/k values and, when normalising,
+        // the matching weights (independent of the data, so off the critical path)
+        f4 a[MAXS], b[MAXS], wa[MAXS], wb[MAXS];
 #pragma unroll
         for (int s = 0; s < MAXS; ++s) {
             const int u = threadIdx.x + s * T;
-            a[s] = f4(0.0f);
-            b[s] = f4(0.0f);
+            a[s] = b[s] = wa[s] = wb[s] = f4(0.0f);
             if (s < slots && u < U) {
                 const int h = u / G;
                 const int i = u % G;
-                const float* src = (h < nq) ? qrow_in + h * HD : krow + (h - nq) * HD;
+                const bool isq = h < nq;
+                const float* src = isq ? qrow_in + h * HD : krow + (h - nq) * HD;
                 a[s] = ld4<true>(src + 4 * i);
                 b[s] = ld4<true>(src + HALF + 4 * i);
+                if constexpr (NORM == kNormRow) {
+                    if (isq) {
+                        wa[s] = ld4<false>(wq + h * HD + 4 * i);
+                        wb[s] = ld4<false>(wq + h * HD + HALF + 4 * i);
+                    }
+                } else if constexpr (NORM == kNormHead) {
+                    const float* wr = isq ? wq : wk;
+                    wa[s] = ld4<false>(wr + 4 * i);
+                    wb[s] = ld4<false>(wr + HALF + 4 * i);
+                }
             }
         }
 
@@ -116,14 +132,12 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
             f4 vb = b[s];
             if constexpr (NORM == kNormRow) {
                 if (isq) {
-                    const float* wr = wq + h * HD;
-                    va = (ld4<false>(wr + 4 * i) * va) * rrow;
-                    vb = (ld4<false>(wr + HALF + 4 * i) * vb) * rrow;
+                    va = (wa[s] * va) * rrow;
+                    vb = (wb[s] * vb) * rrow;
                 }
             } else if constexpr (NORM == kNormHead) {
-                const float* wr = isq ? wq : wk;
-                va = (ld4<false>(wr + 4 * i) * va) * rh[s];
-                vb = (ld4<false>(wr + HALF + 4 * i) * vb) * rh[s];
+                va = (wa[s] * va) * rh[s];
+                vb = (wb[s] * vb) * rh[s];
             }
             if constexpr (ROPE == kRopeNeox) {
                 const f4 c = *reinterpret_cast<const f4*>(cs + 4 * i);
@@ -224,10 +238,7 @@ int dispatch_slots(unsigned grid, unsigned threads, hipStream_t s, float* qo, co
     if (slots <= 1)
         return launch(head_ops_vec_kernel<ROPE, NORM, G, 1>, dim3(grid), dim3(threads), 0, s, qo, qi,
                       k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
-    if (slots <= 2)
-        return launch(head_ops_vec_kernel<ROPE, NORM, G, 2>, dim3(grid), dim3(threads), 0, s, qo, qi,
-                      k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
-    return launch(head_ops_vec_kernel<ROPE, NORM, G, 4>, dim3(grid), dim3(threads), 0, s, qo, qi, k,
+    return launch(head_ops_vec_kernel<ROPE, NORM, G, 2>, dim3(grid), dim3(threads), 0, s, qo, qi, k,
                   wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
 }
 
@@ -338,7 +349,7 @@ int head_ops_launch(float* qo, const float* qi, float* k, const float* wq, const
                ok16(wq) && ok16(wk);
     unsigned threads = 256;
     int slots = 0;
-    if (vec) vec = pick_row_shape(static_cast<int64_t>(nq + nkv) * G, 4, &threads, &slots);
+    if (vec) vec = plan_row(tokens, static_cast<int64_t>(nq + nkv) * G, FENCE_HEAD_SLOTS, 2, &threads, &slots);
     const unsigned grid = grid_1d(tokens, 1, 1 << 20);
     switch (rope) {
         case kRopeNone:

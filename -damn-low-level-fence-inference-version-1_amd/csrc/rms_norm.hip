@@ -3,13 +3,17 @@
 // Follows rms_norm, src/kernels/ops.cuh:17-51:
 //   r = rsqrt(sum(x^2) / n + eps);  out[i] = (w[i] * x[i]) * r.
 // The reference runs one 1024-thread block and reads x twice.  Here one
-// workgroup owns one row; the row is read once with 128-bit loads -- one or
-// two float4 per lane over up to 16 waves -- and kept in VGPRs, the sum of
-// squares is reduced with DPP inside each wave and one LDS exchange across
-// waves, and the normalised row is written from the registers.  out may
-// equal x: every element is read before the reduction's barrier and written
-// after it.
+// workgroup owns one row; the row is read once with 128-bit loads -- about
+// two float4 per lane, all issued before any is consumed -- and kept in
+// VGPRs, the sum of squares is reduced with DPP inside each wave and one LDS
+// exchange across waves, and the normalised row is written from the
+// registers.  out may equal x: every element is read before the reduction's
+// barrier and written after it.
 #include "common.hpp"
+
+#ifndef FENCE_RMS_VPT
+#define FENCE_RMS_VPT 2
+#endif
 
 namespace fence {
 namespace {
@@ -25,25 +29,26 @@ __global__ __launch_bounds__(1024) void rms_rows_vec_kernel(
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const float* xr = x + r * n;
         float* orow = out + r * n;
-        f4 v[MAXV];
-        float ss = 0.0f;
+        f4 v[MAXV], wv[MAXV];
 #pragma unroll
-        for (int j = 0; j < MAXV; ++j) {
+        for (int j = 0; j < MAXV; ++j) {  // the row and its weights, all loads first
             const int f = threadIdx.x + j * T;
+            v[j] = f4(0.0f);
+            wv[j] = f4(0.0f);
             if (j < vpt && f < n4) {
                 v[j] = ld4<true>(xr + 4 * f);
-                ss += dot4(v[j]);
+                wv[j] = ld4<false>(w + 4 * f);
             }
         }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MAXV; ++j) ss += dot4(v[j]);
         const float tot = block_reduce_dyn(ss, OpAdd(), red);
         const float rs = rsqrtf(tot / static_cast<float>(n) + eps);
 #pragma unroll
         for (int j = 0; j < MAXV; ++j) {
             const int f = threadIdx.x + j * T;
-            if (j < vpt && f < n4) {
-                const f4 wv = ld4<false>(w + 4 * f);
-                st4<true>(orow + 4 * f, (wv * v[j]) * rs);
-            }
+            if (j < vpt && f < n4) st4<true>(orow + 4 * f, (wv[j] * v[j]) * rs);
         }
         __syncthreads();  // red[] is rewritten by the next row
     }
@@ -76,7 +81,7 @@ int rms_norm_rows_launch(float* out, const float* x, const float* w, int64_t row
     const bool vec = (n % 4 == 0) && aligned(out, 16) && aligned(x, 16) && aligned(w, 16);
     unsigned threads = 0;
     int vpt = 0;
-    if (vec && pick_row_shape(n / 4, 8, &threads, &vpt)) {
+    if (vec && plan_row(rows, n / 4, FENCE_RMS_VPT, 8, &threads, &vpt)) {
         if (vpt <= 2)
             return launch(rms_rows_vec_kernel<2>, dim3(grid), dim3(threads), 0, s, out, x, w, rows,
                           n, vpt, eps);

@@ -66,6 +66,14 @@ def lib(path: str = LIB_PATH) -> ctypes.CDLL:
     """Load libfence_ops.so once; raise if it has not been built."""
     global _lib
     if _lib is None:
+        # One HIP runtime per process: PyTorch-ROCm ships its own
+        # libamdhip64.so (soname libamdhip64.so.7).  Loading torch first makes
+        # this library bind to that copy; loading it first would pull in a
+        # second runtime that then finds no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(path):
             raise FileNotFoundError(
                 f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
