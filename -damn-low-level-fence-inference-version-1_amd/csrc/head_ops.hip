@@ -49,36 +49,48 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
     const int T = blockDim.x;
     const int U = (nq + nkv) * G;
 
+    // A lane's slots map to the same (head, unit) in every token, so the
+    // norm weights are loaded once per workgroup, before the token loop.
+    f4 wa[MAXS], wb[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+        const int u = threadIdx.x + s * T;
+        wa[s] = wb[s] = f4(0.0f);
+        if (NORM != kNormNone && s < slots && u < U) {
+            const int h = u / G;
+            const int i = u % G;
+            const bool isq = h < nq;
+            if constexpr (NORM == kNormRow) {
+                if (isq) {
+                    wa[s] = ld4<false>(wq + h * HD + 4 * i);
+                    wb[s] = ld4<false>(wq + h * HD + HALF + 4 * i);
+                }
+            } else if constexpr (NORM == kNormHead) {
+                const float* wr = isq ? wq : wk;
+                wa[s] = ld4<false>(wr + 4 * i);
+                wb[s] = ld4<false>(wr + HALF + 4 * i);
+            }
+        }
+    }
+
     for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
         const int pos = positions ? positions[t] : pos0 + static_cast<int>(t);
         const float* qrow_in = qi + t * nq * HD;
         float* qrow_out = qo + t * nq * HD;
         float* krow = k + t * nkv * HD;
 
-        // every load of the lane first: its q/k values and, when normalising,
-        // the matching weights (independent of the data, so off the critical path)
-        f4 a[MAXS], b[MAXS], wa[MAXS], wb[MAXS];
+        // every load of the lane is issued before any is consumed
+        f4 a[MAXS], b[MAXS];
 #pragma unroll
         for (int s = 0; s < MAXS; ++s) {
             const int u = threadIdx.x + s * T;
-            a[s] = b[s] = wa[s] = wb[s] = f4(0.0f);
+            a[s] = b[s] = f4(0.0f);
             if (s < slots && u < U) {
                 const int h = u / G;
                 const int i = u % G;
-                const bool isq = h < nq;
-                const float* src = isq ? qrow_in + h * HD : krow + (h - nq) * HD;
+                const float* src = (h < nq) ? qrow_in + h * HD : krow + (h - nq) * HD;
                 a[s] = ld4<true>(src + 4 * i);
                 b[s] = ld4<true>(src + HALF + 4 * i);
-                if constexpr (NORM == kNormRow) {
-                    if (isq) {
-                        wa[s] = ld4<false>(wq + h * HD + 4 * i);
-                        wb[s] = ld4<false>(wq + h * HD + HALF + 4 * i);
-                    }
-                } else if constexpr (NORM == kNormHead) {
-                    const float* wr = isq ? wq : wk;
-                    wa[s] = ld4<false>(wr + 4 * i);
-                    wb[s] = ld4<false>(wr + HALF + 4 * i);
-                }
             }
         }
 

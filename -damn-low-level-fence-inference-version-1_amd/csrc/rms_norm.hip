@@ -26,19 +26,21 @@ __global__ __launch_bounds__(1024) void rms_rows_vec_kernel(
     __shared__ float red[kMaxWaves];
     const int T = blockDim.x;
     const int n4 = n >> 2;
+    f4 wv[MAXV];  // the weights: the same for every row, loaded once
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+        const int f = threadIdx.x + j * T;
+        wv[j] = (j < vpt && f < n4) ? ld4<false>(w + 4 * f) : f4(0.0f);
+    }
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const float* xr = x + r * n;
         float* orow = out + r * n;
-        f4 v[MAXV], wv[MAXV];
+        f4 v[MAXV];
 #pragma unroll
-        for (int j = 0; j < MAXV; ++j) {  // the row and its weights, all loads first
+        for (int j = 0; j < MAXV; ++j) {  // all loads of the row first
             const int f = threadIdx.x + j * T;
             v[j] = f4(0.0f);
-            wv[j] = f4(0.0f);
-            if (j < vpt && f < n4) {
-                v[j] = ld4<true>(xr + 4 * f);
-                wv[j] = ld4<false>(w + 4 * f);
-            }
+            if (j < vpt && f < n4) v[j] = ld4<true>(xr + 4 * f);
         }
         float ss = 0.0f;
 #pragma unroll
