@@ -16,7 +16,8 @@
 // squares is a DPP reduction inside a 16-lane row (hd = 128).
 // freq[] is computed on the host (exactly the reference expression) and
 // passed in the kernel arguments; cos/sin of the token's hd/2 angles are
-// computed once per token into LDS and shared by all heads.
+// computed once per token into LDS and shared by all heads, while the
+// token's loads are in flight.
 #include "common.hpp"
 
 #include <cmath>
@@ -38,10 +39,22 @@ struct InvFreq {
 
 namespace {
 
+// sin and cos of an angle given in radians as an exact float (the angle
+// (float)pos * freq[p], bit-identical to the reference's).  The angle is
+// divided by pi and reduced to [-1, 1] in double -- error ~1e-16 for angles
+// up to 2^24 rad -- and sincospif finishes in single precision with no
+// large-argument reduction path.
+__device__ __forceinline__ void sincos_angle(float a, float* s, float* c) {
+    double t = static_cast<double>(a) * 0.31830988618379067154;  // 1/pi
+    t -= 2.0 * __builtin_rint(t * 0.5);
+    sincospif(static_cast<float>(t), s, c);
+}
+
+// MAXS units per lane (exactly: the dispatcher launches MAXS == slots).
 template <int ROPE, int NORM, int G, int MAXS>
 __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
     float* qo, const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
-    int nkv, int slots, float eps, const int32_t* positions, int pos0, InvFreq tab) {
+    int nkv, float eps, const int32_t* __restrict__ positions, int pos0, InvFreq tab) {
     constexpr int HD = 8 * G;
     constexpr int HALF = 4 * G;
     __shared__ __align__(16) float cs[2 * HALF];  // cos[HALF] then sin[HALF]
@@ -56,7 +69,7 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
     for (int s = 0; s < MAXS; ++s) {
         const int u = threadIdx.x + s * T;
         wa[s] = wb[s] = f4(0.0f);
-        if (NORM != kNormNone && s < slots && u < U) {
+        if (NORM != kNormNone && u < U) {
             const int h = u / G;
             const int i = u % G;
             const bool isq = h < nq;
@@ -73,34 +86,48 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
         }
     }
 
+    // the lane's pair frequencies (p = lane, lane + T < hd/2), read out of
+    // the kernel arguments once: a lookup issued after the data loads would
+    // make the angle wait for all of them (vmcnt drains in order)
+    float invf[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int p = threadIdx.x + j * T;
+        invf[j] = (ROPE != kRopeNone && p < HALF) ? tab.v[p] : 0.0f;
+    }
+
     for (int64_t t = blockIdx.x; t < tokens; t += gridDim.x) {
         const int pos = positions ? positions[t] : pos0 + static_cast<int>(t);
         const float* qrow_in = qi + t * nq * HD;
         float* qrow_out = qo + t * nq * HD;
         float* krow = k + t * nkv * HD;
 
-        // every load of the lane is issued before any is consumed
+        // Every load of the lane is issued before any is consumed, and without
+        // branches (a lane past the last unit reloads the last unit and drops
+        // the values), so the compiler can count them and start the angles
+        // while they are in flight.
         f4 a[MAXS], b[MAXS];
 #pragma unroll
         for (int s = 0; s < MAXS; ++s) {
-            const int u = threadIdx.x + s * T;
-            a[s] = b[s] = f4(0.0f);
-            if (s < slots && u < U) {
-                const int h = u / G;
-                const int i = u % G;
-                const float* src = (h < nq) ? qrow_in + h * HD : krow + (h - nq) * HD;
-                a[s] = ld4<true>(src + 4 * i);
-                b[s] = ld4<true>(src + HALF + 4 * i);
-            }
+            int u = threadIdx.x + s * T;
+            u = u < U ? u : U - 1;
+            const int h = u / G;
+            const int i = u % G;
+            const float* src = (h < nq) ? qrow_in + h * HD : krow + (h - nq) * HD;
+            a[s] = ld4<true>(src + 4 * i);
+            b[s] = ld4<true>(src + HALF + 4 * i);
         }
 
         if constexpr (ROPE != kRopeNone) {
-            for (int p = threadIdx.x; p < HALF; p += T) {
-                const float ang = static_cast<float>(pos) * tab.v[p];
-                float sn, cn;
-                sincosf(ang, &sn, &cn);
-                cs[p] = cn;
-                cs[HALF + p] = sn;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int p = threadIdx.x + j * T;
+                if (p < HALF) {
+                    float sn, cn;
+                    sincos_angle(static_cast<float>(pos) * invf[j], &sn, &cn);
+                    cs[p] = cn;
+                    cs[HALF + p] = sn;
+                }
             }
         }
 
@@ -110,7 +137,7 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
 #pragma unroll
             for (int s = 0; s < MAXS; ++s) {
                 const int u = threadIdx.x + s * T;
-                if (s < slots && u < nq * G) ss += dot4(a[s]) + dot4(b[s]);
+                if (u < nq * G) ss += dot4(a[s]) + dot4(b[s]);
             }
             const float tot = block_reduce_dyn(ss, OpAdd(), red);
             rrow = rsqrtf(tot / static_cast<float>(nq * HD) + eps);
@@ -120,14 +147,8 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
         if constexpr (NORM == kNormHead) {
 #pragma unroll
             for (int s = 0; s < MAXS; ++s) {
-                float ss = 0.0f;
-                if (s < slots) ss = dot4(a[s]) + dot4(b[s]);
-                if (s < slots) {  // slots is uniform: whole waves enter together
-                    const float tot = group_reduce<G>(ss, OpAdd());
-                    rh[s] = rsqrtf(tot / static_cast<float>(HD) + eps);
-                } else {
-                    rh[s] = 1.0f;
-                }
+                const float tot = group_reduce<G>(dot4(a[s]) + dot4(b[s]), OpAdd());
+                rh[s] = rsqrtf(tot / static_cast<float>(HD) + eps);
             }
         }
 
@@ -136,7 +157,7 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
 #pragma unroll
         for (int s = 0; s < MAXS; ++s) {
             const int u = threadIdx.x + s * T;
-            if (!(s < slots && u < U)) continue;
+            if (u >= U) continue;
             const int h = u / G;
             const int i = u % G;
             const bool isq = h < nq;
@@ -233,7 +254,7 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(
                         x1 = (wr[i1] * x1) * r;
                     }
                     float sn, cn;
-                    sincosf(static_cast<float>(pos) * tab.v[p], &sn, &cn);
+                    sincos_angle(static_cast<float>(pos) * tab.v[p], &sn, &cn);
                     dst[i0] = x0 * cn - x1 * sn;
                     dst[i1] = x0 * sn + x1 * cn;
                 }
@@ -247,11 +268,11 @@ template <int ROPE, int NORM, int G>
 int dispatch_slots(unsigned grid, unsigned threads, hipStream_t s, float* qo, const float* qi,
                    float* k, const float* wq, const float* wk, int64_t tokens, int nq, int nkv,
                    int slots, float eps, const int32_t* positions, int pos0, const InvFreq& tab) {
-    if (slots <= 1)
+    if (slots == 1)
         return launch(head_ops_vec_kernel<ROPE, NORM, G, 1>, dim3(grid), dim3(threads), 0, s, qo, qi,
-                      k, wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+                      k, wq, wk, tokens, nq, nkv, eps, positions, pos0, tab);
     return launch(head_ops_vec_kernel<ROPE, NORM, G, 2>, dim3(grid), dim3(threads), 0, s, qo, qi, k,
-                  wq, wk, tokens, nq, nkv, slots, eps, positions, pos0, tab);
+                  wq, wk, tokens, nq, nkv, eps, positions, pos0, tab);
 }
 
 template <int ROPE, int NORM>
