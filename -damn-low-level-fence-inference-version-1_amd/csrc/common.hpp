@@ -59,10 +59,13 @@ enum : int {
     kDppMirror = 0x140,    // lane i <- lane 15-i within 16
 };
 
+// Every control used here permutes lanes inside a 16-lane row, so with all
+// lanes active no source is out of range and bound_ctrl never applies; setting
+// it lets the compiler fold the move into the consuming VALU op (v_add_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(
-        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
 // xor-16 exchange inside 32-lane halves (ds_swizzle bit mode: and=0x1F, xor=0x10)

@@ -37,6 +37,7 @@ SIGNATURES = {
     "fence_silu_elementwise_mul": (_P, _P, _P, _I, _P),
     "fence_softmax": (_P, _I, _P),
     "fence_embed_q8_0": (_P, _P, _I, _I, _P),
+    "fence_gemv_q8_0": (_P, _P, _P, _I, _I, _P),
     "fence_rms_norm_rows": (_P, _P, _P, _L, _I, _F, _P),
     "fence_rope": (_P, _P, _L, _I, _I, _I, _P, _I, _F, _I, _P),
     "fence_qk_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
@@ -130,6 +131,10 @@ def softmax(x, n, stream=None):
 
 def embed_q8_0(out, weight, token_id, dim, stream=None):
     _call("fence_embed_q8_0", out, weight, token_id, dim, stream)
+
+
+def gemv_q8_0(W, x, y, M, K, stream=None):
+    _call("fence_gemv_q8_0", W, x, y, M, K, stream)
 
 
 def rms_norm_rows(out, x, w, rows, n, eps, stream=None):

@@ -96,6 +96,15 @@ int fence_softmax(float* x, int n, hipStream_t stream);
 int fence_embed_q8_0(float* out, const void* weight, int token_id, int dim,
                      hipStream_t stream);
 
+/* Replaces gemv_q8_0, src/kernels/gemv_q8_0.cuh:99-104 (the tied LM head,
+ * src/model/qwen3.cu:261).  y[M] = W x for a Q8_0 matrix W of M rows of K/32
+ * blocks and fp32 x[K]:  y[r] = sum_b d_b * sum_i qs_b[i] * x[32b + i].
+ * K % 32 == 0 and W 2-byte aligned (block_q8_0 holds an fp16), else
+ * FENCE_EINVAL; K == 0 writes zeros.  Summation order differs from the
+ * reference's; results agree within fp32 rounding of the dot products. */
+int fence_gemv_q8_0(const void* W, const float* x, float* y, int M, int K,
+                    hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Batched and fused forms.  These compose the reference's single-row ops over
  * many tokens (its prefill is a per-token loop, src/model/qwen3.cu:478-481)

@@ -185,6 +185,11 @@ void fo_softmax_causal(float* x, int64_t heads, int sq, int sk) {
 
 /* ------------------------------------------------------------------- Q8_0 */
 
+/* the fp16 scale d of a block, stored little-endian in its first two bytes */
+static float block_scale(const uint8_t* blk) {
+    return fo_fp16_to_f32((uint16_t)(blk[0] | ((uint16_t)blk[1] << 8)));
+}
+
 /* src/kernels/gemv_q8_0.cuh:12-29 with the block layout of
  * src/kernels/q8_0_types.h:10-15: out[i] = half2float(d[i/32]) * qs[i/32][i%32] */
 void fo_embed_q8_0(float* out, const uint8_t* table, int token_id, int dim) {
@@ -192,8 +197,7 @@ void fo_embed_q8_0(float* out, const uint8_t* table, int token_id, int dim) {
     const uint8_t* row = table + (int64_t)token_id * nb * FO_Q8_0_BLOCK_BYTES;
     for (int i = 0; i < dim; ++i) {
         const uint8_t* blk = row + (i / FO_QK8_0) * FO_Q8_0_BLOCK_BYTES;
-        const uint16_t dbits = (uint16_t)(blk[0] | ((uint16_t)blk[1] << 8));
-        const float d = fo_fp16_to_f32(dbits);
+        const float d = block_scale(blk);
         const int8_t q = (int8_t)blk[2 + i % FO_QK8_0];
         out[i] = d * (float)q;
     }
@@ -224,6 +228,26 @@ int64_t fo_embed_q8_0_gather_rms_norm(float* out, const uint8_t* table,
         fo_rms_norm(o, o, w, dim, eps);
     }
     return bad;
+}
+
+/* src/kernels/gemv_q8_0.cuh:40-60 (q8_0_dot_f32_warp_partial) and :75-97:
+ * y[row] = sum_b d_b * (sum_i qs[b][i] * x[32b + i]); the reference sums in
+ * fp32 per lane then across the warp; the oracle accumulates in double. */
+void fo_gemv_q8_0(const uint8_t* W, const float* x, float* y, int M, int K) {
+    const int nb = K / FO_QK8_0;
+    for (int r = 0; r < M; ++r) {
+        const uint8_t* row = W + (int64_t)r * nb * FO_Q8_0_BLOCK_BYTES;
+        double sum = 0.0;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t* blk = row + b * FO_Q8_0_BLOCK_BYTES;
+            const double d = block_scale(blk);
+            double block_sum = 0.0;
+            for (int i = 0; i < FO_QK8_0; ++i)
+                block_sum += (double)(int8_t)blk[2 + i] * (double)x[b * FO_QK8_0 + i];
+            sum += d * block_sum;
+        }
+        y[r] = (float)sum;
+    }
 }
 
 /* ------------------------------------------------------ fused compositions */

@@ -95,6 +95,11 @@ int64_t fo_embed_q8_0_gather_rms_norm(float* out, const uint8_t* table,
                                       int64_t tokens, int dim, const float* w,
                                       float eps);
 
+/* Q8_0 GEMV, y[M] = W[M x K] x[K]: src/kernels/gemv_q8_0.cuh:40-104
+ * (per row: sum over blocks of d * sum_i qs[i] * x[32b+i]), accumulated in
+ * double.  K % 32 == 0. */
+void fo_gemv_q8_0(const uint8_t* W, const float* x, float* y, int M, int K);
+
 /* a7: per-head RMSNorm of q (weight wq[hd]) and k (wk[hd]) then RoPE,
  * per token (src/model/qwen3.cu:293-299 composed). */
 void fo_qk_norm_rope(float* q, float* k, const float* wq, const float* wk,

@@ -371,8 +371,37 @@ def check_fused(o: Oracle):
     return fails
 
 
+# ------------------------------------------------------------------- GEMV
+
+def check_gemv(o: Oracle):
+    fails = []
+    rng = np.random.default_rng(29)
+    M, K = 257, 2560
+    tab = make_q8_0_table(rng, M, K)
+    W = q8_0_dequant_numpy(tab, np.arange(M), K).astype(np.float64)  # independent dequant
+    x = rng.standard_normal(K).astype(np.float32)
+    got = o.gemv_q8_0(tab, x)
+    ref = W @ x.astype(np.float64)
+    scale = np.abs(W) @ np.abs(x.astype(np.float64))  # the dot products' natural error scale
+    err = np.max(np.abs(got - ref) / scale)
+    if not err <= 1e-7:
+        fails.append(f"gemv vs float64 matmul: {err:.3g} of sum|w x| > 1e-7")
+    # a unit vector picks one dequantised column exactly (one nonzero product)
+    for j in (0, 31, 32, 1000, K - 1):
+        e = np.zeros(K, np.float32)
+        e[j] = 1.0
+        col = o.gemv_q8_0(tab, e)
+        if not np.array_equal(col.view(np.uint32), W[:, j].astype(np.float32).view(np.uint32)):
+            fails.append(f"gemv with unit vector e_{j} is not column {j} of the dequantised table")
+            break
+    # linearity: W(2x) = 2 W x exactly (scaling by 2 is exact)
+    if not np.array_equal(o.gemv_q8_0(tab, 2 * x), 2 * got):
+        fails.append("gemv not exactly linear under x -> 2x")
+    return fails
+
+
 ALL_CHECKS = [check_fp16, check_q8_0, check_rms_norm, check_inv_freq, check_rope, check_swiglu,
-              check_softmax, check_fused]
+              check_softmax, check_fused, check_gemv]
 
 
 def run_all(o: Oracle):

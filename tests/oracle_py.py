@@ -40,6 +40,7 @@ _SIGS = {
     "fo_embed_q8_0": ((_P, _P, _I, _I), None),
     "fo_embed_q8_0_gather": ((_P, _P, _L, _P, _L, _I), ctypes.c_int64),
     "fo_embed_q8_0_gather_rms_norm": ((_P, _P, _L, _P, _L, _I, _P, _F), ctypes.c_int64),
+    "fo_gemv_q8_0": ((_P, _P, _P, _I, _I), None),
     "fo_qk_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
     "fo_rms_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
 }
@@ -175,6 +176,15 @@ class Oracle:
         bad = self.lib.fo_embed_q8_0_gather_rms_norm(_ptr(out), _ptr(t), vocab, _ptr(ids), ids.size,
                                                      dim, _ptr(w), eps)
         return out, bad
+
+    def gemv_q8_0(self, table_bytes, x):
+        """y[M] = W[M x K] x[K] for a Q8_0 table [M, K/32*34] bytes."""
+        t = np.ascontiguousarray(table_bytes, dtype=np.uint8)
+        x = _f32(x)
+        M, K = t.shape[0], x.size
+        y = np.empty(M, dtype=np.float32)
+        self.lib.fo_gemv_q8_0(_ptr(t), _ptr(x), _ptr(y), M, K)
+        return y
 
     # fused -----------------------------------------------------------------
     def qk_norm_rope(self, q, k, wq, wk, eps, positions, pos0, base, style):

@@ -75,6 +75,10 @@ def _raw(name):
     ("fence_embed_q8_0_gather", (16, 32, 100, None, 4, 64, None)),
     ("fence_embed_q8_0_gather", (16, 32, 0, 48, 4, 64, None)),    # vocab 0
     ("fence_embed_q8_0_gather_rms_norm", (16, 32, 100, 48, 4, 64, None, 1e-6, None)),
+    ("fence_gemv_q8_0", (16, 32, 48, 8, 48, None)),               # K % 32 != 0
+    ("fence_gemv_q8_0", (0x1001, 32, 48, 8, 64, None)),           # W not 2-byte aligned
+    ("fence_gemv_q8_0", (16, 32, None, 8, 64, None)),
+    ("fence_gemv_q8_0", (16, 32, 48, -1, 64, None)),
 ])
 def test_invalid_arguments_rejected_on_host(fence, name, args):
     assert _raw(name)(*args) == EINVAL
@@ -86,6 +90,7 @@ def test_zero_sized_calls_are_no_ops(fence):
     assert _raw("fence_rope")(16, 32, 0, 4, 2, 128, None, 0, 1e6, 0, None) == 0
     assert _raw("fence_softmax_causal")(16, 0, 4, 4, None) == 0
     assert _raw("fence_embed_q8_0_gather")(16, 32, 10, 48, 0, 64, None) == 0
+    assert _raw("fence_gemv_q8_0")(16, 32, 48, 0, 64, None) == 0
 
 
 @pytest.mark.parametrize("base,hd", [(1e6, 128), (5e5, 128), (5e6, 128), (1e4, 64), (1e6, 256)])

@@ -37,6 +37,8 @@ MUTANTS = [
     ("q8_scale_byte_order", "blk[0] | ((uint16_t)blk[1] << 8)", "blk[1] | ((uint16_t)blk[0] << 8)"),
     ("fp16_subnormal_scale", "(float)man * 0x1p-24f", "(float)man * 0x1p-23f"),
     ("fp16_exponent_bias", "((exp + 112u) << 23)", "((exp + 111u) << 23)"),
+    ("gemv_drops_scale", "sum += d * block_sum;", "sum += block_sum;"),
+    ("gemv_x_offset_off_by_one", "(double)x[b * FO_QK8_0 + i]", "(double)x[b * FO_QK8_0 + i + (i < 31)]"),
     ("qk_norm_k_uses_q_weight", "fo_rms_norm_per_head(k + t * krow, wk,", "fo_rms_norm_per_head(k + t * krow, wq,"),
 ]
 
