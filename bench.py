@@ -19,7 +19,8 @@ recording HIP events at its own kernel start and end
 (fence_time_next_launch -> hipExtLaunchKernel, on the launch stream: the
 interval a kernel-trace profiler reports); the roofline of the dominant
 kernel (swiglu) from K such launches;
-the Llama-3-8B decode-step op set in microseconds, a device-copy
+the Llama-3-8B decode-step op set in microseconds, the Q8_0 LM-head GEMV
+(128256 x 4096, once per decoded token), a device-copy
 calibration, and the CPU baseline (the scalar oracle on one host core,
 timed on a bounded sample of the same step).
 """
@@ -72,6 +73,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--decode-reps", type=int, default=300)
+    ap.add_argument("--lm-head-reps", type=int, default=60,
+                    help="launches of the Q8_0 LM-head GEMV pass (0 skips it)")
     ap.add_argument("--all", metavar="PATH", default=None,
                     help="also measure every op of BASELINE.json configs[0..4] and write the "
                          "per-op report (JSON) to PATH; a table goes to stderr")
@@ -281,6 +284,7 @@ def main():
                           "pass after the timed region, same cold buffer rotation"}
 
     decode = decode_op_set(torch, F, gen, args.decode_reps)
+    lm_head = lm_head_gemv(torch, F, gen, args.lm_head_reps)
     copy_gbps = copy_calibration(torch)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -313,11 +317,44 @@ def main():
         "ops": per_op,
         "roofline": roofline,
         "decode_op_set_llama3_8b": decode,
+        "lm_head_gemv_q8_0": lm_head,
         "copy_calibration_GBps": copy_gbps,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 4),
     }
     print(json.dumps(line), flush=True)
+
+
+def lm_head_gemv(torch, F, gen, reps):
+    """The tied LM head of a decode step at configs[1] shape (qwen3.cu:261):
+    logits[128256] = W x over the Q8_0 table [128256 x 4096], one launch per
+    token.  Each launch records its own kernel start/end; three tables
+    (1.67 GB) rotate so no launch finds its table in the Infinity Cache."""
+    if reps <= 0:
+        return None
+    hev = HipEvents()
+    sh = torch.cuda.current_stream().cuda_stream
+    tables = [make_q8_0_table(torch, gen, VOCAB, HIDDEN) for _ in range(3)]
+    x = torch.randn(HIDDEN, device="cuda", generator=gen)
+    y = torch.empty(VOCAB, device="cuda")
+    for i in range(3):
+        F.gemv_q8_0(tables[i].data_ptr(), x.data_ptr(), y.data_ptr(), VOCAB, HIDDEN, sh)
+    evs = [(hev.create(), hev.create()) for _ in range(reps)]
+    for i in range(reps):
+        F.time_next_launch(*evs[i])
+        F.gemv_q8_0(tables[i % 3].data_ptr(), x.data_ptr(), y.data_ptr(), VOCAB, HIDDEN, sh)
+    torch.cuda.synchronize()
+    ts = sorted(hev.elapsed_ms(a, b) * 1e3 for a, b in evs)
+    hev.destroy_all()
+    del tables
+    torch.cuda.empty_cache()
+    mean = sum(ts) / len(ts)
+    nbytes = gemv_bytes(VOCAB, HIDDEN)
+    return {"shape": [VOCAB, HIDDEN], "bytes": nbytes, "us_mean": round(mean, 3),
+            "us_p50": round(ts[len(ts) // 2], 3), "us_p10": round(ts[len(ts) // 10], 3),
+            "GBps": round(nbytes / (mean * 1e-6) / 1e9, 1),
+            "frac_peak": round(nbytes / (mean * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+            "kernel": "gemv_q8_0_staged_kernel", "launches": reps}
 
 
 def decode_op_set(torch, F, gen, reps):
@@ -407,6 +444,11 @@ def decode_op_set(torch, F, gen, reps):
     return out
 
 
+def gemv_bytes(m, k):
+    """Algorithmic bytes of y[m] = W x over a Q8_0 W: the table once, x, y."""
+    return m * (k // 32) * 34 + 4 * k + 4 * m
+
+
 def all_configs(torch, F, path, reps):
     """Every op of BASELINE.json configs[0..4] on seeded synthetic inputs.
     Each launch records its own kernel start/end; inputs rotate over enough
@@ -482,6 +524,10 @@ def all_configs(torch, F, path, reps):
     measure(0, "embed_q8_0 1 id x 2560", E0 * 4 + E0 // 32 * 34 + 4,
             lambda: dict(o=torch.empty(E0, **dev)), embed0)
     del tab0
+    # tied LM head (qwen3.cu:261): the whole table is read once per decoded token
+    measure(0, f"gemv_q8_0 lm head {V0}x{E0}", gemv_bytes(V0, E0),
+            lambda: dict(t=make_q8_0_table(torch, gen, V0, E0), x=randn(E0), y=torch.empty(V0, **dev)),
+            lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V0, E0, sh))
 
     # ---- Llama-3-8B prefill T=512 (the bench step's ops)
     T1, H1, F1, V1 = 512, 4096, 14336, 128256
@@ -499,6 +545,9 @@ def all_configs(torch, F, path, reps):
                          o=torch.empty(T1, H1, **dev)),
             lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), T1, H1, sh))
     del tab1
+    measure(1, f"gemv_q8_0 lm head {V1}x{H1}", gemv_bytes(V1, H1),
+            lambda: dict(t=make_q8_0_table(torch, gen, V1, H1), x=randn(H1), y=torch.empty(V1, **dev)),
+            lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V1, H1, sh))
 
     # ---- Qwen3-8B long prefill T=4096
     T2, F2 = 4096, 12288

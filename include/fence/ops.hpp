@@ -68,4 +68,10 @@ inline void embed_q8_0(float* d_out, const block_q8_0* d_weight, int token_id, i
     fence_detail::record(fence_embed_q8_0(d_out, d_weight, token_id, dim, stream));
 }
 
+/* src/kernels/gemv_q8_0.cuh:99 */
+inline void gemv_q8_0(const block_q8_0* d_W, const float* d_x, float* d_y, int M, int K,
+                      hipStream_t stream = 0) {
+    fence_detail::record(fence_gemv_q8_0(d_W, d_x, d_y, M, K, stream));
+}
+
 #endif /* FENCE_OPS_HPP */

@@ -1,7 +1,8 @@
 // decode_layer.cpp -- the drop-in check.  One decode step's hot-path calls,
 // made through the reference's own launcher names (include/fence/ops.hpp) in
 // the order src/model/qwen3.cu makes them (forward :246, forward_attention
-// :274-299, gqa softmax :357-391, forward_mlp :324-332, final norm :257), at
+// :274-299, gqa softmax :357-391, forward_mlp :324-332, final norm :257,
+// tied LM head :261), at
 // Qwen3-4B shapes, each output checked against the CPU oracle.
 // Prints one PASS/FAIL line per check and exits with the number of failures.
 #include "fence/ops.hpp"
@@ -180,7 +181,34 @@ int main() {
     fo_rms_norm_inplace(f_ref.data(), w_out.data(), E, eps);
     check_rows("rms_norm_inplace(output)", hidden.get(), f_ref, E);
 
-    // 8. error behaviour: a null pointer launches nothing and leaves EINVAL
+    // 8. tied LM head over the final hidden state (qwen3.cu:261): per row
+    //    |y - y_ref| <= 1e-5 * sum_j |W_rj x_j|, the scale of a dot product's rounding
+    {
+        Dev logits(V);
+        gemv_q8_0(d_table, hidden.p, logits.p, V, E);
+        const auto fin = hidden.get();
+        std::vector<float> l_ref(V);
+        fo_gemv_q8_0(reinterpret_cast<const uint8_t*>(table.data()), fin.data(), l_ref.data(), V, E);
+        const auto lg = logits.get();
+        double worst = 0.0, maxabs = 0.0;
+        bool ok = true;
+        for (int r = 0; r < V; ++r) {
+            double scale = 0.0;
+            for (size_t b = 0; b < nb; ++b) {
+                const block_q8_0& blk = table[static_cast<size_t>(r) * nb + b];
+                const double d = std::fabs(static_cast<double>(__half2float(blk.d)));
+                for (int i = 0; i < 32; ++i)
+                    scale += d * std::abs(static_cast<int>(blk.qs[i])) * std::fabs(static_cast<double>(fin[b * 32 + i]));
+            }
+            const double err = std::fabs(static_cast<double>(lg[r]) - static_cast<double>(l_ref[r]));
+            if (!(err <= 1e-5 * scale)) ok = false;
+            worst = std::fmax(worst, scale > 0 ? err / scale : err);
+            maxabs = std::fmax(maxabs, err);
+        }
+        report("gemv_q8_0 (tied LM head, err/sum|wx|)", ok, worst, maxabs);
+    }
+
+    // 9. error behaviour: a null pointer launches nothing and leaves EINVAL
     rms_norm(nullptr, hidden.p, out_norm.p, E, eps);
     report("invalid launch reports EINVAL", fence_last_status() == FENCE_ERROR_INVALID_VALUE, 0, 0);
     rms_norm(normed.p, hidden.p, out_norm.p, E, eps);
