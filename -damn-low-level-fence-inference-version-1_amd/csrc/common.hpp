@@ -37,6 +37,22 @@ __device__ __forceinline__ void st4(float* p, f4 v) {
     else *reinterpret_cast<f4*>(p) = v;
 }
 
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+// binary32 -> binary16 by the hardware conversion (v_cvt_f16_f32): round to
+// nearest even, overflow to inf, binary16 subnormals kept (the default MODE).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// Four binary16 values rounded from a float4, one 64-bit store (p 8-byte aligned).
+template <bool NT>
+__device__ __forceinline__ void st_h4(uint16_t* p, f4 v) {
+    const h4 h = __builtin_convertvector(v, h4);
+    if constexpr (NT) __builtin_nontemporal_store(h, reinterpret_cast<h4*>(p));
+    else *reinterpret_cast<h4*>(p) = h;
+}
+
 __device__ __forceinline__ float dot4(f4 a) {
     // pairwise: (a0^2 + a1^2) + (a2^2 + a3^2)
     return (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);

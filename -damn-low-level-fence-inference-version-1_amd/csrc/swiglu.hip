@@ -1,4 +1,5 @@
-// swiglu.hip -- out = silu(gate) * up on gfx950.
+// swiglu.hip -- out = silu(gate) * up on gfx950, in fp32 and/or rounded to
+// binary16 for the next GEMV's input.
 //
 // Follows silu_elementwise_mul, src/kernels/ops.cuh:183-202:
 //   out[i] = (g / (1.0f + expf(-g))) * up[i],  g = gate[i].
@@ -21,9 +22,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
-template <int UNROLL>
+// OUT32: fp32 result to `out`; OUT16: its binary16 rounding to `out16`
+// (the f32_to_f16 that src/model/qwen3.cu:336 runs as a separate pass).
+template <int UNROLL, bool OUT32, bool OUT16>
 __global__ __launch_bounds__(kSwigluThreads) void swiglu_vec_kernel(
-    float* out, const float* gate, const float* up, int64_t n4) {
+    float* out, uint16_t* out16, const float* gate, const float* up, int64_t n4) {
     const int64_t base = static_cast<int64_t>(blockIdx.x) * (kSwigluThreads * UNROLL) + threadIdx.x;
     f4 g[UNROLL], u[UNROLL];
 #pragma unroll
@@ -43,25 +46,40 @@ __global__ __launch_bounds__(kSwigluThreads) void swiglu_vec_kernel(
             r.y = silu_mul(g[j].y, u[j].y);
             r.z = silu_mul(g[j].z, u[j].z);
             r.w = silu_mul(g[j].w, u[j].w);
-            st4<true>(out + 4 * i, r);
+            if constexpr (OUT32) st4<true>(out + 4 * i, r);
+            if constexpr (OUT16) st_h4<true>(out16 + 4 * i, r);
         }
     }
 }
 
-// Scalar form for unaligned pointers and the n % 4 tail.
+// Scalar form for unaligned pointers and the n % 4 tail; out or out16 may be null.
 __global__ __launch_bounds__(kSwigluThreads) void swiglu_scalar_kernel(
-    float* out, const float* gate, const float* up, int64_t begin, int64_t n) {
+    float* out, uint16_t* out16, const float* gate, const float* up, int64_t begin, int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kSwigluThreads;
     for (int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kSwigluThreads + threadIdx.x; i < n;
-         i += stride)
-        out[i] = silu_mul(gate[i], up[i]);
+         i += stride) {
+        const float r = silu_mul(gate[i], up[i]);
+        if (out) out[i] = r;
+        if (out16) out16[i] = f32_to_f16_bits(r);
+    }
 }
 
-int swiglu_launch(float* out, const float* gate, const float* up, int64_t n, hipStream_t s) {
-    if (!out || !gate || !up || n < 0) return FENCE_ERROR_INVALID_VALUE;
-    if (!aligned(out, 4) || !aligned(gate, 4) || !aligned(up, 4)) return FENCE_ERROR_INVALID_VALUE;
+template <bool OUT32, bool OUT16>
+int launch_swiglu_vec(unsigned grid, hipStream_t s, float* out, uint16_t* out16, const float* gate,
+                      const float* up, int64_t n4) {
+    return launch(swiglu_vec_kernel<kSwigluUnroll, OUT32, OUT16>, dim3(grid), dim3(kSwigluThreads), 0, s,
+                  out, out16, gate, up, n4);
+}
+
+// out or out16 may be null, not both.
+int swiglu_launch(float* out, uint16_t* out16, const float* gate, const float* up, int64_t n,
+                  hipStream_t s) {
+    if ((!out && !out16) || !gate || !up || n < 0) return FENCE_ERROR_INVALID_VALUE;
+    if ((out && !aligned(out, 4)) || (out16 && !aligned(out16, 2)) || !aligned(gate, 4) || !aligned(up, 4))
+        return FENCE_ERROR_INVALID_VALUE;
     if (n == 0) return FENCE_SUCCESS;
-    const bool vec = aligned(out, 16) && aligned(gate, 16) && aligned(up, 16);
+    const bool vec = (!out || aligned(out, 16)) && (!out16 || aligned(out16, 8)) && aligned(gate, 16) &&
+                     aligned(up, 16);
     int64_t done = 0;
     if (vec) {
         const int64_t n4 = n / 4;
@@ -69,15 +87,17 @@ int swiglu_launch(float* out, const float* gate, const float* up, int64_t n, hip
             const unsigned grid = grid_1d(n4, kSwigluThreads * kSwigluUnroll, int64_t(1) << 31);
             if (static_cast<int64_t>(grid) * kSwigluThreads * kSwigluUnroll < n4)
                 return FENCE_ERROR_INVALID_VALUE;  // beyond 2^31 workgroups
-            const int st = launch(swiglu_vec_kernel<kSwigluUnroll>, dim3(grid), dim3(kSwigluThreads),
-                                  0, s, out, gate, up, n4);
+            int st;
+            if (out && !out16) st = launch_swiglu_vec<true, false>(grid, s, out, out16, gate, up, n4);
+            else if (!out) st = launch_swiglu_vec<false, true>(grid, s, out, out16, gate, up, n4);
+            else st = launch_swiglu_vec<true, true>(grid, s, out, out16, gate, up, n4);
             if (st) return st;
         }
         done = n4 * 4;
     }
     if (done < n) {
         const unsigned grid = grid_1d(n - done, kSwigluThreads, 65536);
-        return launch(swiglu_scalar_kernel, dim3(grid), dim3(kSwigluThreads), 0, s, out, gate, up,
+        return launch(swiglu_scalar_kernel, dim3(grid), dim3(kSwigluThreads), 0, s, out, out16, gate, up,
                       done, n);
     }
     return FENCE_SUCCESS;
@@ -88,11 +108,18 @@ int swiglu_launch(float* out, const float* gate, const float* up, int64_t n, hip
 
 extern "C" int fence_swiglu(float* out, const float* gate, const float* up, int64_t n,
                             hipStream_t stream) {
-    return fence::swiglu_launch(out, gate, up, n, stream);
+    if (!out) return FENCE_ERROR_INVALID_VALUE;
+    return fence::swiglu_launch(out, nullptr, gate, up, n, stream);
 }
 
 extern "C" int fence_silu_elementwise_mul(float* out, const float* gate, const float* up, int n,
                                           hipStream_t stream) {
-    if (n < 0) return FENCE_ERROR_INVALID_VALUE;
-    return fence::swiglu_launch(out, gate, up, n, stream);
+    if (!out || n < 0) return FENCE_ERROR_INVALID_VALUE;
+    return fence::swiglu_launch(out, nullptr, gate, up, n, stream);
+}
+
+extern "C" int fence_swiglu_f16(void* out_f16, float* out, const float* gate, const float* up,
+                                int64_t n, hipStream_t stream) {
+    if (!out_f16) return FENCE_ERROR_INVALID_VALUE;
+    return fence::swiglu_launch(out, static_cast<uint16_t*>(out_f16), gate, up, n, stream);
 }

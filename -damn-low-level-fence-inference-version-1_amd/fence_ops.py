@@ -38,6 +38,11 @@ SIGNATURES = {
     "fence_softmax": (_P, _I, _P),
     "fence_embed_q8_0": (_P, _P, _I, _I, _P),
     "fence_gemv_q8_0": (_P, _P, _P, _I, _I, _P),
+    "fence_residual_add": (_P, _P, _I, _P),
+    "fence_f32_to_f16": (_P, _P, _I, _P),
+    "fence_f16_to_f32": (_P, _P, _I, _P),
+    "fence_residual_rms_norm_f16": (_P, _P, _P, _P, _P, _L, _I, _F, _P),
+    "fence_swiglu_f16": (_P, _P, _P, _P, _L, _P),
     "fence_rms_norm_rows": (_P, _P, _P, _L, _I, _F, _P),
     "fence_rope": (_P, _P, _L, _I, _I, _I, _P, _I, _F, _I, _P),
     "fence_qk_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
@@ -135,6 +140,26 @@ def embed_q8_0(out, weight, token_id, dim, stream=None):
 
 def gemv_q8_0(W, x, y, M, K, stream=None):
     _call("fence_gemv_q8_0", W, x, y, M, K, stream)
+
+
+def residual_add(x, residual, n, stream=None):
+    _call("fence_residual_add", x, residual, n, stream)
+
+
+def f32_to_f16(out, inp, n, stream=None):
+    _call("fence_f32_to_f16", out, inp, n, stream)
+
+
+def f16_to_f32(out, inp, n, stream=None):
+    _call("fence_f16_to_f32", out, inp, n, stream)
+
+
+def residual_rms_norm_f16(hidden, residual, w, normed, out_f16, rows, n, eps, stream=None):
+    _call("fence_residual_rms_norm_f16", hidden, residual, w, normed, out_f16, rows, n, eps, stream)
+
+
+def swiglu_f16(out_f16, out, gate, up, n, stream=None):
+    _call("fence_swiglu_f16", out_f16, out, gate, up, n, stream)
 
 
 def rms_norm_rows(out, x, w, rows, n, eps, stream=None):

@@ -524,6 +524,21 @@ def all_configs(torch, F, path, reps):
     measure(0, "embed_q8_0 1 id x 2560", E0 * 4 + E0 // 32 * 34 + 4,
             lambda: dict(o=torch.empty(E0, **dev)), embed0)
     del tab0
+    # layer-boundary epilogue (qwen3.cu:310-325): fused, and the reference's separate passes
+    h16 = dict(dtype=torch.int16, device="cuda")
+    measure(0, "residual->rms_norm->f16 2560 (fused)", E0 * (4 + 4 + 4 + 2 + 4),
+            lambda: dict(h=randn(E0), r=randn(E0), w=1 + 0.1 * randn(E0), o=torch.empty(E0, **h16)),
+            lambda b: F.residual_rms_norm_f16(b["h"].data_ptr(), b["r"].data_ptr(), b["w"].data_ptr(), None,
+                                              b["o"].data_ptr(), 1, E0, 1e-6, sh))
+    measure(0, "residual_add 2560 (unfused part)", 3 * E0 * 4,
+            lambda: dict(h=randn(E0), r=randn(E0)),
+            lambda b: F.residual_add(b["h"].data_ptr(), b["r"].data_ptr(), E0, sh))
+    measure(0, "f32_to_f16 2560 (unfused part)", E0 * 6,
+            lambda: dict(x=randn(E0), o=torch.empty(E0, **h16)),
+            lambda b: F.f32_to_f16(b["o"].data_ptr(), b["x"].data_ptr(), E0, sh))
+    measure(0, "swiglu->f16 9728 (fused)", F0 * 10,
+            lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **h16)),
+            lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), F0, sh))
     # tied LM head (qwen3.cu:261): the whole table is read once per decoded token
     measure(0, f"gemv_q8_0 lm head {V0}x{E0}", gemv_bytes(V0, E0),
             lambda: dict(t=make_q8_0_table(torch, gen, V0, E0), x=randn(E0), y=torch.empty(V0, **dev)),
@@ -545,6 +560,14 @@ def all_configs(torch, F, path, reps):
                          o=torch.empty(T1, H1, **dev)),
             lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), T1, H1, sh))
     del tab1
+    h16 = dict(dtype=torch.int16, device="cuda")
+    measure(1, "residual->rms_norm->f16 512x4096", T1 * H1 * (4 + 4 + 4 + 2) + 4 * H1,
+            lambda: dict(h=randn(T1, H1), r=randn(T1, H1), o=torch.empty(T1, H1, **h16)),
+            lambda b: F.residual_rms_norm_f16(b["h"].data_ptr(), b["r"].data_ptr(), w1.data_ptr(), None,
+                                              b["o"].data_ptr(), T1, H1, 1e-5, sh))
+    measure(1, "swiglu->f16 512x14336", T1 * F1 * (4 + 4 + 2),
+            lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **h16)),
+            lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh))
     measure(1, f"gemv_q8_0 lm head {V1}x{H1}", gemv_bytes(V1, H1),
             lambda: dict(t=make_q8_0_table(torch, gen, V1, H1), x=randn(H1), y=torch.empty(V1, **dev)),
             lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V1, H1, sh))
@@ -604,6 +627,9 @@ def all_configs(torch, F, path, reps):
     measure(4, "swiglu 8192x14336", 3 * T4 * F4 * 4,
             lambda: dict(g=randn(T4, F4), u=randn(T4, F4), o=torch.empty(T4, F4, **dev)),
             lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T4 * F4, sh))
+    measure(4, "swiglu->f16 8192x14336", T4 * F4 * (4 + 4 + 2),
+            lambda: dict(g=randn(T4, F4), u=randn(T4, F4), o=torch.empty(T4, F4, dtype=torch.int16, **dev)),
+            lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), T4 * F4, sh))
     measure(4, "rope interleaved Q+K 8192x(32+8)x128", 2 * T4 * 40 * 128 * 4,
             lambda: dict(q=randn(T4, 32 * 128), k=randn(T4, 8 * 128)),
             lambda b: F.rope(b["q"].data_ptr(), b["k"].data_ptr(), T4, 32, 8, 128, None, 0, 1e6,

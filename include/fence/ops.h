@@ -105,6 +105,18 @@ int fence_embed_q8_0(float* out, const void* weight, int token_id, int dim,
 int fence_gemv_q8_0(const void* W, const float* x, float* y, int M, int K,
                     hipStream_t stream);
 
+/* Replaces residual_add, src/kernels/ops.cuh:265-270: x[i] += residual[i]. */
+int fence_residual_add(float* x, const float* residual, int n, hipStream_t stream);
+
+/* Replaces f32_to_f16, src/kernels/ops.cuh:457-462, and float_to_half,
+ * :284-289 (the same operation): out[i] = binary16(in[i]), round to nearest
+ * even, overflow to inf, NaN to a quiet NaN.  out holds n binary16 values
+ * (__half / _Float16), 2-byte aligned. */
+int fence_f32_to_f16(void* out, const float* in, int n, hipStream_t stream);
+
+/* Replaces half_to_float, src/kernels/ops.cuh:303-308: out[i] = in[i] (exact). */
+int fence_f16_to_f32(float* out, const void* in, int n, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Batched and fused forms.  These compose the reference's single-row ops over
  * many tokens (its prefill is a per-token loop, src/model/qwen3.cu:478-481)
@@ -180,6 +192,23 @@ int fence_embed_q8_0_gather_rms_norm(float* out, const void* table,
 /* inv_freq[p] = 1.0f / powf(freq_base, (float)(2p) / (float)head_dim) for
  * p < head_dim/2 (src/kernels/ops.cuh:133), computed on the host: the RoPE
  * kernels receive exactly these values. */
+/* The layer-boundary epilogue (src/model/qwen3.cu:310-325: residual_add,
+ * the copy to the residual buffer, rms_norm, f32_to_f16) in one pass, on
+ * `rows` rows of n:  hidden += residual (skipped if residual is NULL; the sum
+ * stays in hidden, which is also the next residual);  normed = rms_norm(hidden,
+ * w, eps);  out_f16 = binary16(normed) (round to nearest even).  normed or
+ * out_f16 may be NULL, not both; normed must not be hidden when residual is
+ * given.  Without a residual it is qwen3.cu:274-278 (rms_norm, f32_to_f16). */
+int fence_residual_rms_norm_f16(float* hidden, const float* residual, const float* w,
+                                float* normed, void* out_f16, int64_t rows, int n,
+                                float eps, hipStream_t stream);
+
+/* SwiGLU with its conversion for the down projection (src/model/qwen3.cu:
+ * 332-336): act = silu(gate) * up; out_f16 = binary16(act); out (fp32 act) may
+ * be NULL. */
+int fence_swiglu_f16(void* out_f16, float* out, const float* gate, const float* up,
+                     int64_t n, hipStream_t stream);
+
 int fence_rope_inv_freq(float* inv_freq, int head_dim, float freq_base);
 
 /* Kernel timing: the next kernel this host thread launches through this

@@ -74,4 +74,24 @@ inline void gemv_q8_0(const block_q8_0* d_W, const float* d_x, float* d_y, int M
     fence_detail::record(fence_gemv_q8_0(d_W, d_x, d_y, M, K, stream));
 }
 
+/* src/kernels/ops.cuh:265 */
+inline void residual_add(float* x, const float* residual, int n, hipStream_t stream = 0) {
+    fence_detail::record(fence_residual_add(x, residual, n, stream));
+}
+
+/* src/kernels/ops.cuh:457 */
+inline void f32_to_f16(half* out, const float* in, int n, hipStream_t stream = 0) {
+    fence_detail::record(fence_f32_to_f16(out, in, n, stream));
+}
+
+/* src/kernels/ops.cuh:284 */
+inline void float_to_half(half* out, const float* in, int n, hipStream_t stream = 0) {
+    fence_detail::record(fence_f32_to_f16(out, in, n, stream));
+}
+
+/* src/kernels/ops.cuh:303 */
+inline void half_to_float(float* out, const half* in, int n, hipStream_t stream = 0) {
+    fence_detail::record(fence_f16_to_f32(out, in, n, stream));
+}
+
 #endif /* FENCE_OPS_HPP */

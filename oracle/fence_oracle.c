@@ -250,6 +250,72 @@ void fo_gemv_q8_0(const uint8_t* W, const float* x, float* y, int M, int K) {
     }
 }
 
+/* ------------------------------------------------- f16 and residual epilogue */
+
+/* src/kernels/ops.cuh:448-462 (f32_to_f16) and :274-289 (float_to_half):
+ * out[i] = __float2half(in[i]), IEEE round to nearest even. */
+uint16_t fo_f32_to_f16(float f) {
+    const uint32_t b = f32_to_bits(f);
+    const uint32_t sign = (b >> 16) & 0x8000u;
+    const uint32_t exp = (b >> 23) & 0xFFu;
+    const uint32_t man = b & 0x7FFFFFu;
+    if (exp == 0xFFu) /* inf, or NaN made quiet */
+        return (uint16_t)(sign | 0x7C00u | (man ? 0x0200u | (man >> 13) : 0u));
+    if (exp >= 113u) { /* normal in binary16 unless rounding carries past 65504 */
+        const uint32_t e16 = exp - 112u;
+        if (e16 >= 31u) return (uint16_t)(sign | 0x7C00u);
+        uint32_t h = (e16 << 10) | (man >> 13);
+        const uint32_t rem = man & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u; /* a carry may reach inf */
+        return (uint16_t)(sign | h);
+    }
+    /* binary16 subnormal or zero: value = sig * 2^(exp-150), unit 2^-24 */
+    const uint32_t shift = 126u - exp; /* >= 14 */
+    if (exp == 0u || shift > 24u) return (uint16_t)sign;
+    const uint32_t sig = man | 0x800000u;
+    uint32_t q = sig >> shift;
+    const uint32_t rem = sig & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q += 1u;
+    return (uint16_t)(sign | q);
+}
+
+void fo_f32_to_f16_array(uint16_t* out, const float* in, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = fo_f32_to_f16(in[i]);
+}
+
+/* src/kernels/ops.cuh:256-270 */
+void fo_residual_add(float* x, const float* residual, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] += residual[i];
+}
+
+/* src/model/qwen3.cu:312 then :318-325 (residual_add; rms_norm; f32_to_f16) */
+void fo_residual_rms_norm_f16(float* hidden, const float* residual, const float* w,
+                              float* normed, uint16_t* out16, int64_t rows, int n,
+                              float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float* h = hidden + r * n;
+        if (residual) fo_residual_add(h, residual + r * n, n);
+        const float rs = rms_scale(h, n, eps);
+        for (int i = 0; i < n; ++i) {
+            const float v = (w[i] * h[i]) * rs;
+            if (normed) normed[r * n + i] = v;
+            if (out16) out16[r * n + i] = fo_f32_to_f16(v);
+        }
+    }
+}
+
+/* src/model/qwen3.cu:332-336 (silu_elementwise_mul; f32_to_f16) */
+void fo_swiglu_f16(uint16_t* out16, float* out, const float* gate, const float* up,
+                   int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float v;
+        fo_silu_elementwise_mul(&v, gate + i, up + i, 1);
+        if (out) out[i] = v;
+        out16[i] = fo_f32_to_f16(v);
+    }
+}
+
 /* ------------------------------------------------------ fused compositions */
 
 void fo_qk_norm_rope(float* q, float* k, const float* wq, const float* wk,

@@ -100,6 +100,25 @@ int64_t fo_embed_q8_0_gather_rms_norm(float* out, const uint8_t* table,
  * double.  K % 32 == 0. */
 void fo_gemv_q8_0(const uint8_t* W, const float* x, float* y, int M, int K);
 
+/* IEEE binary32 -> binary16, round to nearest, ties to even; overflow -> inf;
+ * NaN -> quiet NaN of the same sign.  The reference's __float2half in
+ * f32_to_f16 (src/kernels/ops.cuh:448-462) and float_to_half (:274-289). */
+uint16_t fo_f32_to_f16(float f);
+void fo_f32_to_f16_array(uint16_t* out, const float* in, int64_t n);
+/* residual_add, src/kernels/ops.cuh:256-270: x[i] += residual[i] */
+void fo_residual_add(float* x, const float* residual, int64_t n);
+/* The layer-boundary epilogue of src/model/qwen3.cu:310-325 (and :272-278
+ * without a residual), per row of n: hidden += residual (if residual),
+ * normed = rms_norm(hidden, w), out16 = f32_to_f16(normed).  normed and out16
+ * may each be NULL. */
+void fo_residual_rms_norm_f16(float* hidden, const float* residual, const float* w,
+                              float* normed, uint16_t* out16, int64_t rows, int n,
+                              float eps);
+/* src/model/qwen3.cu:332-336: act = silu(gate) * up; out16 = f32_to_f16(act);
+ * out (fp32 act) may be NULL. */
+void fo_swiglu_f16(uint16_t* out16, float* out, const float* gate, const float* up,
+                   int64_t n);
+
 /* a7: per-head RMSNorm of q (weight wq[hd]) and k (wk[hd]) then RoPE,
  * per token (src/model/qwen3.cu:293-299 composed). */
 void fo_qk_norm_rope(float* q, float* k, const float* wq, const float* wk,

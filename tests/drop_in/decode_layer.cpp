@@ -137,6 +137,20 @@ int main() {
     fo_rms_norm(n_ref.data(), h.data(), w_attn.data(), E, eps);
     check_rows("rms_norm(attn)", normed.get(), n_ref, E);
 
+    // 2b. the GEMV input conversion (qwen3.cu:278), bit-exact on the device's normed row
+    {
+        const auto dn = normed.get();
+        half* x_half = nullptr;
+        HIP_CHECK(hipMalloc(&x_half, E * sizeof(half)));
+        f32_to_f16(x_half, normed.p, E);
+        std::vector<uint16_t> got16(E), want16(E);
+        HIP_CHECK(hipDeviceSynchronize());
+        HIP_CHECK(hipMemcpy(got16.data(), x_half, E * 2, hipMemcpyDeviceToHost));
+        fo_f32_to_f16_array(want16.data(), dn.data(), E);
+        report("f32_to_f16 (bit-exact)", got16 == want16, 0, 0);
+        HIP_CHECK(hipFree(x_half));
+    }
+
     // 3. QK-norm (qwen3.cu:293-294) on synthetic projections
     auto hq = normals(rng, NQ * HD), hk = normals(rng, NKV * HD);
     q.put(hq); k.put(hk);
@@ -174,6 +188,18 @@ int main() {
     silu_elementwise_mul(gate.p, gate.p, up.p, FF);
     fo_silu_elementwise_mul(hg.data(), hg.data(), hu.data(), FF);
     check_rows("silu_elementwise_mul(out == gate)", gate.get(), hg, FF);
+
+    // 6b. the sub-block's residual add (qwen3.cu:338), bit-exact
+    {
+        auto hres = normals(rng, E);
+        Dev res(E), sum(E);
+        res.put(hres);
+        sum.put(h);
+        residual_add(sum.p, res.p, E);
+        std::vector<float> want(h);
+        fo_residual_add(want.data(), hres.data(), E);
+        check_bits("residual_add (bit-exact)", sum.get(), want);
+    }
 
     // 7. final norm in place (qwen3.cu:257)
     rms_norm_inplace(hidden.p, out_norm.p, E, eps);

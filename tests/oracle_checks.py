@@ -400,8 +400,88 @@ def check_gemv(o: Oracle):
     return fails
 
 
+# ------------------------------------------------------- f16 and epilogue
+
+def f32_patterns(rng):
+    """float32 bit patterns over every exponent: mantissas at and around the
+    binary16 rounding point (13 dropped bits), random mantissas, and for the
+    binary16-subnormal exponents the exact halfway cases of each shift."""
+    mans = [0, 1, 0xFFF, 0x1000, 0x1001, 0x1FFF, 0x2000, 0x3000, 0x5000, 0x7FE000, 0x7FEFFF,
+            0x7FF000, 0x7FF001, 0x7FFFFF, 0x400000]
+    pats = []
+    for e in range(256):
+        ms = np.concatenate([np.array(mans, np.uint32), rng.integers(0, 1 << 23, 48, dtype=np.uint32)])
+        pats.append((np.uint32(e) << 23) | ms)
+    for e in range(100, 113):  # binary16 subnormal results: shift = 126 - e in [14, 26]
+        shift = 126 - e
+        k = rng.integers(0, 1 << max(1, 24 - shift), 32, dtype=np.uint32)
+        sig = (k << np.uint32(shift)) | np.uint32(1 << (shift - 1))
+        sig = sig | np.uint32(0x800000)
+        pats.append((np.uint32(e) << 23) | (sig & np.uint32(0x7FFFFF)))
+    p = np.concatenate(pats)
+    return np.concatenate([p, p | np.uint32(0x80000000)])
+
+
+def check_f16_epilogue(o: Oracle):
+    fails = []
+    rng = np.random.default_rng(41)
+    bits = f32_patterns(rng)
+    x = bits.view(np.float32)
+    got = o.f32_to_f16(x)
+    nan = np.isnan(x)
+    with np.errstate(over="ignore"):
+        ref = x[~nan].astype(np.float16).view(np.uint16)
+    if not np.array_equal(got[~nan], ref):
+        bad = np.nonzero(got[~nan] != ref)[0][:3]
+        fails.append(f"f32->f16 differs from numpy's RNE at {[hex(int(b)) for b in bits[~nan][bad]]}")
+    gn = got[nan]
+    if not np.all(((gn & 0x7C00) == 0x7C00) & ((gn & 0x3FF) != 0)):
+        fails.append("f32->f16 of NaN is not a NaN")
+    # every binary16 value survives f16 -> f32 -> f16 (NaNs come back quiet)
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    back = o.f32_to_f16(h.view(np.float16).astype(np.float32))
+    hn = np.isnan(h.view(np.float16))
+    if not np.array_equal(back[~hn], h[~hn]):
+        fails.append("f16 -> f32 -> f16 is not the identity")
+    # closed forms at the edges of the binary16 range
+    cases = {65504.0: 0x7BFF, 65519.99: 0x7BFF, 65520.0: 0x7C00, 2.0 ** -24: 0x0001, 2.0 ** -25: 0x0000,
+             1.5 * 2.0 ** -25: 0x0001, 2.0 ** -14: 0x0400, 1.0 + 2.0 ** -11: 0x3C00,
+             1.0 + 3 * 2.0 ** -11: 0x3C02, -0.0: 0x8000}
+    for v, want in cases.items():
+        g = int(o.f32_to_f16(np.array([v], np.float32))[0])
+        if g != want:
+            fails.append(f"f32->f16({v!r}) = {g:#06x}, want {want:#06x}")
+    # residual add is a plain fp32 add
+    a = rng.standard_normal(1000).astype(np.float32)
+    b = rng.standard_normal(1000).astype(np.float32)
+    if not np.array_equal(o.residual_add(a, b), a + b):
+        fails.append("residual_add differs from numpy's fp32 add")
+    # the fused epilogue equals its pinned parts, bit for bit
+    hid = rng.standard_normal((3, 640)).astype(np.float32)
+    res = rng.standard_normal((3, 640)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(640)).astype(np.float32)
+    h2, normed, o16 = o.residual_rms_norm_f16(hid, res, w, 1e-6)
+    if not np.array_equal(h2, hid + res):
+        fails.append("epilogue: hidden is not hidden + residual")
+    if not np.array_equal(normed, o.rms_norm_rows(hid + res, w, 1e-6)):
+        fails.append("epilogue: normed differs from rms_norm of the sum")
+    if not np.array_equal(o16, normed.astype(np.float16).view(np.uint16)):
+        fails.append("epilogue: f16 output is not RNE of the normed row")
+    h3, normed3, _ = o.residual_rms_norm_f16(hid, None, w, 1e-6)
+    if not (np.array_equal(h3, hid) and np.array_equal(normed3, o.rms_norm_rows(hid, w, 1e-6))):
+        fails.append("epilogue without residual: hidden changed or norm differs")
+    g = rng.standard_normal(999).astype(np.float32)
+    u = rng.standard_normal(999).astype(np.float32)
+    act, a16 = o.swiglu_f16(g, u)
+    if not np.array_equal(act, o.silu_mul(g, u)):
+        fails.append("swiglu_f16: fp32 output differs from silu_elementwise_mul")
+    if not np.array_equal(a16, act.astype(np.float16).view(np.uint16)):
+        fails.append("swiglu_f16: f16 output is not RNE of the fp32 output")
+    return fails
+
+
 ALL_CHECKS = [check_fp16, check_q8_0, check_rms_norm, check_inv_freq, check_rope, check_swiglu,
-              check_softmax, check_fused, check_gemv]
+              check_softmax, check_fused, check_gemv, check_f16_epilogue]
 
 
 def run_all(o: Oracle):

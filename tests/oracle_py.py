@@ -41,6 +41,11 @@ _SIGS = {
     "fo_embed_q8_0_gather": ((_P, _P, _L, _P, _L, _I), ctypes.c_int64),
     "fo_embed_q8_0_gather_rms_norm": ((_P, _P, _L, _P, _L, _I, _P, _F), ctypes.c_int64),
     "fo_gemv_q8_0": ((_P, _P, _P, _I, _I), None),
+    "fo_f32_to_f16": ((_F,), ctypes.c_uint16),
+    "fo_f32_to_f16_array": ((_P, _P, _L), None),
+    "fo_residual_add": ((_P, _P, _L), None),
+    "fo_residual_rms_norm_f16": ((_P, _P, _P, _P, _P, _L, _I, _F), None),
+    "fo_swiglu_f16": ((_P, _P, _P, _P, _L), None),
     "fo_qk_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
     "fo_rms_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
 }
@@ -185,6 +190,42 @@ class Oracle:
         y = np.empty(M, dtype=np.float32)
         self.lib.fo_gemv_q8_0(_ptr(t), _ptr(x), _ptr(y), M, K)
         return y
+
+    # f16 and residual epilogue -------------------------------------------
+    def f32_to_f16(self, x):
+        """binary16 bit patterns (uint16) of float32 values, RNE."""
+        x = _f32(x)
+        out = np.empty(x.shape, dtype=np.uint16)
+        self.lib.fo_f32_to_f16_array(_ptr(out), _ptr(x), x.size)
+        return out
+
+    def residual_add(self, x, residual):
+        x = _f32(x)
+        r = _f32(residual)
+        self.lib.fo_residual_add(_ptr(x), _ptr(r), x.size)
+        return x
+
+    def residual_rms_norm_f16(self, hidden, residual, w, eps):
+        """Returns (hidden after the add, normed fp32, normed as binary16 bits)."""
+        h = _f32(hidden)
+        n = h.shape[-1]
+        rows = h.size // n
+        r = None if residual is None else _f32(residual)
+        w = _f32(w)
+        normed = np.empty(h.shape, np.float32)
+        out16 = np.empty(h.shape, np.uint16)
+        self.lib.fo_residual_rms_norm_f16(_ptr(h), _ptr(r), _ptr(w), _ptr(normed), _ptr(out16),
+                                          rows, n, eps)
+        return h, normed, out16
+
+    def swiglu_f16(self, gate, up):
+        """Returns (fp32 silu(gate) * up, its binary16 bits)."""
+        g = _f32(gate)
+        u = _f32(up)
+        out = np.empty(g.shape, np.float32)
+        out16 = np.empty(g.shape, np.uint16)
+        self.lib.fo_swiglu_f16(_ptr(out16), _ptr(out), _ptr(g), _ptr(u), g.size)
+        return out, out16
 
     # fused -----------------------------------------------------------------
     def qk_norm_rope(self, q, k, wq, wk, eps, positions, pos0, base, style):

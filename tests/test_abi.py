@@ -79,6 +79,15 @@ def _raw(name):
     ("fence_gemv_q8_0", (0x1001, 32, 48, 8, 64, None)),           # W not 2-byte aligned
     ("fence_gemv_q8_0", (16, 32, None, 8, 64, None)),
     ("fence_gemv_q8_0", (16, 32, 48, -1, 64, None)),
+    ("fence_residual_add", (16, None, 8, None)),
+    ("fence_residual_add", (BAD, 32, 8, None)),
+    ("fence_f32_to_f16", (0x1001, 32, 8, None)),                  # binary16 output not 2-byte aligned
+    ("fence_f16_to_f32", (16, 32, -1, None)),
+    ("fence_residual_rms_norm_f16", (16, 32, 48, None, None, 2, 64, 1e-6, None)),  # no output
+    ("fence_residual_rms_norm_f16", (16, 32, 48, 16, None, 2, 64, 1e-6, None)),    # normed == hidden
+    ("fence_residual_rms_norm_f16", (16, 32, 48, 64, 80, 2, 0, 1e-6, None)),
+    ("fence_swiglu_f16", (None, 16, 32, 48, 8, None)),
+    ("fence_swiglu_f16", (0x1001, None, 32, 48, 8, None)),
 ])
 def test_invalid_arguments_rejected_on_host(fence, name, args):
     assert _raw(name)(*args) == EINVAL
@@ -91,6 +100,10 @@ def test_zero_sized_calls_are_no_ops(fence):
     assert _raw("fence_softmax_causal")(16, 0, 4, 4, None) == 0
     assert _raw("fence_embed_q8_0_gather")(16, 32, 10, 48, 0, 64, None) == 0
     assert _raw("fence_gemv_q8_0")(16, 32, 48, 0, 64, None) == 0
+    assert _raw("fence_residual_add")(16, 32, 0, None) == 0
+    assert _raw("fence_f32_to_f16")(16, 32, 0, None) == 0
+    assert _raw("fence_residual_rms_norm_f16")(16, 32, 48, None, 64, 0, 64, 1e-6, None) == 0
+    assert _raw("fence_swiglu_f16")(16, None, 32, 48, 0, None) == 0
 
 
 @pytest.mark.parametrize("base,hd", [(1e6, 128), (5e5, 128), (5e6, 128), (1e4, 64), (1e6, 256)])

@@ -39,6 +39,10 @@ MUTANTS = [
     ("fp16_exponent_bias", "((exp + 112u) << 23)", "((exp + 111u) << 23)"),
     ("gemv_drops_scale", "sum += d * block_sum;", "sum += block_sum;"),
     ("gemv_x_offset_off_by_one", "(double)x[b * FO_QK8_0 + i]", "(double)x[b * FO_QK8_0 + i + (i < 31)]"),
+    ("f16_ties_away_not_even", "(rem == 0x1000u && (h & 1u))", "(rem == 0x1000u)"),
+    ("f16_subnormal_shift", "const uint32_t shift = 126u - exp;", "const uint32_t shift = 127u - exp;"),
+    ("residual_overwrites", "x[i] += residual[i];", "x[i] = residual[i];"),
+    ("epilogue_f16_of_unnormed", "out16[r * n + i] = fo_f32_to_f16(v);", "out16[r * n + i] = fo_f32_to_f16(h[i]);"),
     ("qk_norm_k_uses_q_weight", "fo_rms_norm_per_head(k + t * krow, wk,", "fo_rms_norm_per_head(k + t * krow, wq,"),
 ]
 
