@@ -193,9 +193,9 @@ int fence_embed_q8_0_gather_rms_norm(float* out, const void* table,
  * p < head_dim/2 (src/kernels/ops.cuh:133), computed on the host: the RoPE
  * kernels receive exactly these values. */
 /* The layer-boundary epilogue (src/model/qwen3.cu:310-325: residual_add,
- * the copy to the residual buffer, rms_norm, f32_to_f16) in one pass, on
- * `rows` rows of n:  hidden += residual (skipped if residual is NULL; the sum
- * stays in hidden, which is also the next residual);  normed = rms_norm(hidden,
+ * rms_norm, f32_to_f16) in one pass, on `rows` rows of n:
+ * hidden += residual (skipped if residual is NULL; the sum stays in hidden and
+ * is the next sub-block's residual);  normed = rms_norm(hidden,
  * w, eps);  out_f16 = binary16(normed) (round to nearest even).  normed or
  * out_f16 may be NULL, not both; normed must not be hidden when residual is
  * given.  Without a residual it is qwen3.cu:274-278 (rms_norm, f32_to_f16). */
