@@ -250,6 +250,43 @@ void fo_gemv_q8_0(const uint8_t* W, const float* x, float* y, int M, int K) {
     }
 }
 
+/* ------------------------------------------------------------------- Q6_K */
+
+/* src/kernels/q6k_dot.cuh:35-64: element i of a block sits in half i/128,
+ * column (i%128)/32, lane l = i%32: its low nibble is ql[64*half + l (+32 for
+ * columns 1 and 3)], the low or high nibble (columns 0-1 / 2-3); its two high
+ * bits are bits 2*column of qh[32*half + l]. */
+int fo_q6k_quant(const uint8_t* blk, int i) {
+    const int half = i / 128, col = (i % 128) / 32, l = i % 32;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int lo = (ql[64 * half + l + ((col & 1) ? 32 : 0)] >> ((col >= 2) ? 4 : 0)) & 0xF;
+    const int hi = (qh[32 * half + l] >> (2 * col)) & 0x3;
+    return lo | (hi << 4);
+}
+
+double fo_q6k_dot(const uint8_t* blk, const uint16_t* x16) {
+    const int8_t* scales = (const int8_t*)(blk + 192);
+    const double d = fo_fp16_to_f32((uint16_t)(blk[208] | ((uint16_t)blk[209] << 8)));
+    double sum = 0.0;
+    for (int i = 0; i < FO_QK_K; ++i)
+        sum += d * (double)scales[i / 16] * (double)(fo_q6k_quant(blk, i) - 32) *
+               (double)fo_fp16_to_f32(x16[i]);
+    return sum;
+}
+
+/* src/kernels/gemv_q6k.cuh:44-84 (and :107-138 with the bias) */
+void fo_gemv_q6k(const uint8_t* W, const uint16_t* x16, const float* bias, float* y,
+                 int M, int K) {
+    const int nb = K / FO_QK_K;
+    for (int r = 0; r < M; ++r) {
+        double sum = 0.0;
+        for (int b = 0; b < nb; ++b)
+            sum += fo_q6k_dot(W + ((int64_t)r * nb + b) * FO_Q6K_BLOCK_BYTES, x16 + b * FO_QK_K);
+        y[r] = bias ? (float)sum + bias[r] : (float)sum;
+    }
+}
+
 /* ------------------------------------------------- f16 and residual epilogue */
 
 /* src/kernels/ops.cuh:448-462 (f32_to_f16) and :274-289 (float_to_half):

@@ -100,6 +100,23 @@ int64_t fo_embed_q8_0_gather_rms_norm(float* out, const uint8_t* table,
  * double.  K % 32 == 0. */
 void fo_gemv_q8_0(const uint8_t* W, const float* x, float* y, int M, int K);
 
+/* Q6_K super-block: ql[128] low nibbles, qh[64] high crumbs, int8 scales[16],
+ * fp16 d; 210 bytes, 256 weights.  src/kernels/q6k_types.h:24-35. */
+#define FO_QK_K 256
+#define FO_Q6K_BLOCK_BYTES 210
+
+/* The 6-bit quant of element i (0..63), src/kernels/q6k_dot.cuh:35-64. */
+int fo_q6k_quant(const uint8_t* blk, int i);
+/* dot(block, x[256]) with x as binary16 bit patterns, summed exactly in
+ * double: sum_i d * scales[i/16] * (q6[i] - 32) * x[i]
+ * (src/kernels/q6k_dot.cuh:28-72; the reference tests' CPU golden,
+ * tests/test_q6k_dot.cu:40-83). */
+double fo_q6k_dot(const uint8_t* blk, const uint16_t* x16);
+/* y[M] = W[M x K] x[K] (+ bias[M] if bias), W rows of K/256 Q6_K blocks, x
+ * binary16, y fp32: src/kernels/gemv_q6k.cuh:44-151.  K % 256 == 0. */
+void fo_gemv_q6k(const uint8_t* W, const uint16_t* x16, const float* bias, float* y,
+                 int M, int K);
+
 /* IEEE binary32 -> binary16, round to nearest, ties to even; overflow -> inf;
  * NaN -> quiet NaN of the same sign.  The reference's __float2half in
  * f32_to_f16 (src/kernels/ops.cuh:448-462) and float_to_half (:274-289). */

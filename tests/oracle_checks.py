@@ -14,7 +14,8 @@ import os
 
 import numpy as np
 
-from oracle_py import INTERLEAVED, NEOX, Oracle, make_q8_0_table, q8_0_dequant_numpy
+from oracle_py import (INTERLEAVED, NEOX, Oracle, make_q6k_matrix, make_q8_0_table, q6k_dequant_numpy,
+                       q6k_pack, q8_0_dequant_numpy)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -480,8 +481,57 @@ def check_f16_epilogue(o: Oracle):
     return fails
 
 
+# ------------------------------------------------------------------- Q6_K
+
+def check_q6k(o: Oracle):
+    fails = []
+    fx = np.load(os.path.join(GOLDEN, "q6k_reference_tests.npz"))
+    # the reference's dot tests (tests/test_q6k_dot.cu TC1-TC6): closed forms
+    # exactly, the random TC4 against the independent float64 dequant
+    got = np.array([o.q6k_dot(b, x) for b, x in zip(fx["dot_blocks"], fx["dot_x"])])
+    closed = fx["dot_closed"]
+    known = ~np.isnan(closed)
+    if not np.array_equal(got[known], closed[known]):
+        fails.append(f"q6k dot closed forms (TC1-3, 5, 6): {got[known]} != {closed[known]}")
+    if not np.allclose(got, fx["dot_expected"], rtol=1e-13, atol=1e-12):
+        fails.append("q6k dot differs from the reference tests' vectors")
+    # the reference's GEMV tests (tests/test_gemv_q6k.cu synthetic 64x256, 128x512)
+    for name, K in (("small", 256), ("multi", 512)):
+        W, x, ref = fx[f"{name}_W"], fx[f"{name}_x"], fx[f"{name}_expected"]
+        y = o.gemv_q6k(W, x)
+        scale = np.abs(q6k_dequant_numpy(W, K)) @ np.abs(x.view(np.float16).astype(np.float64))
+        if not np.all(np.abs(y - ref) <= 1e-7 * scale):
+            fails.append(f"q6k gemv {name}: differs from the reference test's vector")
+    # every quant decodes: pack known values with the ggml-style encoder
+    rng = np.random.default_rng(17)
+    q6 = rng.integers(0, 64, (4, 256))
+    blk = q6k_pack(q6, rng.integers(-128, 128, (4, 16)), np.full(4, 0x3C00, np.uint16))
+    for b in range(4):
+        if not np.array_equal(o.q6k_quants(blk[b]), q6[b]):
+            fails.append("q6k quant layout: decode(pack(q)) != q")
+            break
+    # a random matrix against float64 matmul; unit vectors select a column; bias adds in fp32
+    W = make_q6k_matrix(rng, 37, 1024)
+    x = rng.standard_normal(1024).astype(np.float16)
+    deq = q6k_dequant_numpy(W, 1024)
+    y = o.gemv_q6k(W, x.view(np.uint16))
+    ref = deq @ x.astype(np.float64)
+    if not np.all(np.abs(y - ref) <= 1e-7 * (np.abs(deq) @ np.abs(x.astype(np.float64)))):
+        fails.append("q6k gemv vs float64 matmul")
+    for j in (0, 15, 16, 31, 32, 127, 128, 255, 256, 1023):
+        e = np.zeros(1024, np.float16)
+        e[j] = 1.0
+        if not np.array_equal(o.gemv_q6k(W, e.view(np.uint16)), deq[:, j].astype(np.float32)):
+            fails.append(f"q6k gemv with e_{j} is not column {j}")
+            break
+    bias = rng.standard_normal(37).astype(np.float32)
+    if not np.array_equal(o.gemv_q6k(W, x.view(np.uint16), bias), y + bias):
+        fails.append("q6k gemv bias is not an fp32 add of the sum")
+    return fails
+
+
 ALL_CHECKS = [check_fp16, check_q8_0, check_rms_norm, check_inv_freq, check_rope, check_swiglu,
-              check_softmax, check_fused, check_gemv, check_f16_epilogue]
+              check_softmax, check_fused, check_gemv, check_f16_epilogue, check_q6k]
 
 
 def run_all(o: Oracle):

@@ -46,6 +46,9 @@ _SIGS = {
     "fo_residual_add": ((_P, _P, _L), None),
     "fo_residual_rms_norm_f16": ((_P, _P, _P, _P, _P, _L, _I, _F), None),
     "fo_swiglu_f16": ((_P, _P, _P, _P, _L), None),
+    "fo_q6k_quant": ((_P, _I), ctypes.c_int),
+    "fo_q6k_dot": ((_P, _P), ctypes.c_double),
+    "fo_gemv_q6k": ((_P, _P, _P, _P, _I, _I), None),
     "fo_qk_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
     "fo_rms_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
 }
@@ -191,6 +194,27 @@ class Oracle:
         self.lib.fo_gemv_q8_0(_ptr(t), _ptr(x), _ptr(y), M, K)
         return y
 
+    # Q6_K -------------------------------------------------------------------
+    def q6k_quants(self, blk):
+        """The 256 6-bit quants (0..63) of one 210-byte block."""
+        b = np.ascontiguousarray(blk, dtype=np.uint8)
+        return np.array([self.lib.fo_q6k_quant(_ptr(b), i) for i in range(256)], np.int32)
+
+    def q6k_dot(self, blk, x16):
+        b = np.ascontiguousarray(blk, dtype=np.uint8)
+        x = np.ascontiguousarray(x16, dtype=np.uint16)
+        return float(self.lib.fo_q6k_dot(_ptr(b), _ptr(x)))
+
+    def gemv_q6k(self, W, x16, bias=None):
+        """y = W x (+ bias) for W [M, K/256*210] bytes and binary16 x [K]."""
+        w = np.ascontiguousarray(W, dtype=np.uint8)
+        x = np.ascontiguousarray(x16, dtype=np.uint16)
+        M, K = w.shape[0], x.size
+        bz = None if bias is None else _f32(bias)
+        y = np.empty(M, np.float32)
+        self.lib.fo_gemv_q6k(_ptr(w), _ptr(x), _ptr(bz), _ptr(y), M, K)
+        return y
+
     # f16 and residual epilogue -------------------------------------------
     def f32_to_f16(self, x):
         """binary16 bit patterns (uint16) of float32 values, RNE."""
@@ -273,3 +297,55 @@ def q8_0_dequant_numpy(table_bytes: np.ndarray, ids, dim: int) -> np.ndarray:
     q = rows[:, :, 2:].copy().view(np.int8).astype(np.float32)      # [T, nb, 32]
     with np.errstate(invalid="ignore"):  # inf scale * 0 -> NaN, as in fp32
         return (d * q).reshape(-1, dim)
+
+
+# ---------------------------------------------------------------- Q6_K data
+
+def q6k_dequant_numpy(W: np.ndarray, K: int) -> np.ndarray:
+    """Independent Q6_K dequantisation in float64, written as ggml's
+    dequantize_row_q6_K loop (per half of 128: ql[l], ql[l+32] low/high
+    nibbles and the four crumbs of qh[l] give elements l, l+32, l+64, l+96),
+    not as the reference's per-element index arithmetic the oracle follows."""
+    blk = np.ascontiguousarray(W, np.uint8).reshape(-1, 210)
+    ql, qh = blk[:, 0:128].astype(np.int32), blk[:, 128:192].astype(np.int32)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float64)
+    d = blk[:, 208:210].copy().view(np.float16).astype(np.float64)  # [nblk, 1]
+    out = np.empty((blk.shape[0], 256), np.float64)
+    for h in range(2):
+        a, b, c = ql[:, 64 * h:64 * h + 32], ql[:, 64 * h + 32:64 * h + 64], qh[:, 32 * h:32 * h + 32]
+        q = [(a & 0xF) | ((c & 3) << 4), (b & 0xF) | (((c >> 2) & 3) << 4),
+             (a >> 4) | (((c >> 4) & 3) << 4), (b >> 4) | (((c >> 6) & 3) << 4)]
+        for col in range(4):
+            for half16 in range(2):
+                s_idx = 8 * h + 2 * col + half16
+                l = slice(16 * half16, 16 * half16 + 16)
+                out[:, 128 * h + 32 * col + 16 * half16:128 * h + 32 * col + 16 * half16 + 16] = (
+                    d * sc[:, s_idx:s_idx + 1] * (q[col][:, l] - 32))
+    return out.reshape(np.asarray(W).shape[0], -1)[:, :K] if np.asarray(W).ndim == 2 else out.reshape(-1)
+
+
+def q6k_pack(q6: np.ndarray, scales: np.ndarray, d16: np.ndarray) -> np.ndarray:
+    """Blocks [n, 210] from quants [n, 256] (0..63), int8 scales [n, 16] and
+    binary16 d bits [n] -- the inverse of the layout above."""
+    q6 = np.asarray(q6, np.int32)
+    n = q6.shape[0]
+    blk = np.zeros((n, 210), np.uint8)
+    for h in range(2):
+        cols = [q6[:, 128 * h + 32 * c:128 * h + 32 * c + 32] for c in range(4)]
+        blk[:, 64 * h:64 * h + 32] = (cols[0] & 0xF) | ((cols[2] & 0xF) << 4)
+        blk[:, 64 * h + 32:64 * h + 64] = (cols[1] & 0xF) | ((cols[3] & 0xF) << 4)
+        blk[:, 128 + 32 * h:128 + 32 * h + 32] = ((cols[0] >> 4) | ((cols[1] >> 4) << 2) |
+                                                  ((cols[2] >> 4) << 4) | ((cols[3] >> 4) << 6))
+    blk[:, 192:208] = np.asarray(scales, np.int8).view(np.uint8)
+    blk[:, 208:210] = np.asarray(d16, np.uint16).reshape(n, 1).view(np.uint8)
+    return blk
+
+
+def make_q6k_matrix(rng: np.random.Generator, M: int, K: int) -> np.ndarray:
+    """Synthetic Q6_K rows [M, K/256*210]: quants uniform 0..63, scales uniform
+    in [-32, 31], d = binary16(|N(0, 1)| / 4096)."""
+    nb = K // 256
+    q6 = rng.integers(0, 64, (M * nb, 256))
+    sc = rng.integers(-32, 32, (M * nb, 16))
+    d = (np.abs(rng.standard_normal(M * nb)) / 4096).astype(np.float16).view(np.uint16)
+    return q6k_pack(q6, sc, d).reshape(M, nb * 210)

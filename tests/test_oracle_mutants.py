@@ -43,6 +43,11 @@ MUTANTS = [
     ("f16_subnormal_shift", "const uint32_t shift = 126u - exp;", "const uint32_t shift = 127u - exp;"),
     ("residual_overwrites", "x[i] += residual[i];", "x[i] = residual[i];"),
     ("epilogue_f16_of_unnormed", "out16[r * n + i] = fo_f32_to_f16(v);", "out16[r * n + i] = fo_f32_to_f16(h[i]);"),
+    ("q6k_ql_offset_wrong_columns", "l + ((col & 1) ? 32 : 0)", "l + ((col >= 2) ? 32 : 0)"),
+    ("q6k_qh_shift", "(qh[32 * half + l] >> (2 * col)) & 0x3", "(qh[32 * half + l] >> col) & 0x3"),
+    ("q6k_sub_block_32", "(double)scales[i / 16]", "(double)scales[i / 32]"),
+    ("q6k_offset_31", "(fo_q6k_quant(blk, i) - 32)", "(fo_q6k_quant(blk, i) - 31)"),
+    ("q6k_bias_dropped", "y[r] = bias ? (float)sum + bias[r] : (float)sum;", "y[r] = (float)sum;"),
     ("qk_norm_k_uses_q_weight", "fo_rms_norm_per_head(k + t * krow, wk,", "fo_rms_norm_per_head(k + t * krow, wq,"),
 ]
 
