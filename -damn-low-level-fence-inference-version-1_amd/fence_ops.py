@@ -38,6 +38,8 @@ SIGNATURES = {
     "fence_softmax": (_P, _I, _P),
     "fence_embed_q8_0": (_P, _P, _I, _I, _P),
     "fence_gemv_q8_0": (_P, _P, _P, _I, _I, _P),
+    "fence_gemv_q6k": (_P, _P, _P, _I, _I, _P),
+    "fence_gemv_q6k_bias": (_P, _P, _P, _P, _I, _I, _P),
     "fence_residual_add": (_P, _P, _I, _P),
     "fence_f32_to_f16": (_P, _P, _I, _P),
     "fence_f16_to_f32": (_P, _P, _I, _P),
@@ -140,6 +142,14 @@ def embed_q8_0(out, weight, token_id, dim, stream=None):
 
 def gemv_q8_0(W, x, y, M, K, stream=None):
     _call("fence_gemv_q8_0", W, x, y, M, K, stream)
+
+
+def gemv_q6k(W, x, y, M, K, stream=None):
+    _call("fence_gemv_q6k", W, x, y, M, K, stream)
+
+
+def gemv_q6k_bias(W, x, bias, y, M, K, stream=None):
+    _call("fence_gemv_q6k_bias", W, x, bias, y, M, K, stream)
 
 
 def residual_add(x, residual, n, stream=None):

@@ -444,6 +444,20 @@ def decode_op_set(torch, F, gen, reps):
     return out
 
 
+def make_q6k_table(torch, gen, rows, k):
+    """Q6_K rows [rows, k/256*210] with random quants and scales and d = 2^-8."""
+    nb = k // 256
+    t = torch.randint(0, 256, (rows, nb, 210), dtype=torch.uint8, device="cuda", generator=gen)
+    t[:, :, 208] = 0x00
+    t[:, :, 209] = 0x1C  # binary16 2^-8: finite sums
+    return t.view(rows, nb * 210)
+
+
+def q6k_bytes(m, k):
+    """Algorithmic bytes of y[m] = W x over a Q6_K W: the matrix once, binary16 x, fp32 y."""
+    return m * (k // 256) * 210 + 2 * k + 4 * m
+
+
 def gemv_bytes(m, k):
     """Algorithmic bytes of y[m] = W x over a Q8_0 W: the table once, x, y."""
     return m * (k // 32) * 34 + 4 * k + 4 * m
@@ -539,6 +553,14 @@ def all_configs(torch, F, path, reps):
     measure(0, "swiglu->f16 9728 (fused)", F0 * 10,
             lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **h16)),
             lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), F0, sh))
+    # Q6_K projections of one Qwen3-4B decode layer (qwen3.cu:281-337), x in binary16
+    for pname, (pm, pk) in (("q", (4096, 2560)), ("k/v", (1024, 2560)), ("o", (2560, 4096)),
+                            ("gate/up", (9728, 2560)), ("down", (2560, 9728))):
+        measure(0, f"gemv_q6k {pname} {pm}x{pk}", q6k_bytes(pm, pk),
+                lambda pm=pm, pk=pk: dict(W=make_q6k_table(torch, gen, pm, pk), x=randn(pk).half(),
+                                          y=torch.empty(pm, **dev)),
+                lambda b, pm=pm, pk=pk: F.gemv_q6k(b["W"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(),
+                                                   pm, pk, sh))
     # tied LM head (qwen3.cu:261): the whole table is read once per decoded token
     measure(0, f"gemv_q8_0 lm head {V0}x{E0}", gemv_bytes(V0, E0),
             lambda: dict(t=make_q8_0_table(torch, gen, V0, E0), x=randn(E0), y=torch.empty(V0, **dev)),
@@ -568,6 +590,12 @@ def all_configs(torch, F, path, reps):
     measure(1, "swiglu->f16 512x14336", T1 * F1 * (4 + 4 + 2),
             lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **h16)),
             lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh))
+    for pname, (pm, pk) in (("q", (4096, 4096)), ("gate/up", (14336, 4096)), ("down", (4096, 14336))):
+        measure(1, f"gemv_q6k {pname} {pm}x{pk}", q6k_bytes(pm, pk),
+                lambda pm=pm, pk=pk: dict(W=make_q6k_table(torch, gen, pm, pk), x=randn(pk).half(),
+                                          y=torch.empty(pm, **dev)),
+                lambda b, pm=pm, pk=pk: F.gemv_q6k(b["W"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(),
+                                                   pm, pk, sh))
     measure(1, f"gemv_q8_0 lm head {V1}x{H1}", gemv_bytes(V1, H1),
             lambda: dict(t=make_q8_0_table(torch, gen, V1, H1), x=randn(H1), y=torch.empty(V1, **dev)),
             lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V1, H1, sh))

@@ -105,6 +105,20 @@ int fence_embed_q8_0(float* out, const void* weight, int token_id, int dim,
 int fence_gemv_q8_0(const void* W, const float* x, float* y, int M, int K,
                     hipStream_t stream);
 
+/* Replaces gemv_q6k, src/kernels/gemv_q6k.cuh:89-102 (every projection of a
+ * decode step, src/model/qwen3.cu:281-337).  y[M] = W x for a Q6_K matrix W
+ * of M rows of K/256 blocks (block_q6_K, 210 bytes) and binary16 x[K]:
+ *   y[r] = sum_b d_b * sum_i scales_b[i/16] * (q6_b[i] - 32) * x[256b + i].
+ * K % 256 == 0, W and x 2-byte aligned, else FENCE_ERROR_INVALID_VALUE. */
+int fence_gemv_q6k(const void* W, const void* x, float* y, int M, int K,
+                   hipStream_t stream);
+
+/* Replaces gemv_q6k_bias, src/kernels/gemv_q6k.cuh:140-151:
+ * y[r] = (W x)[r] + bias[r] (fp32 add), for the q/k/v biases of
+ * src/model/qwen3.cu:280-287. */
+int fence_gemv_q6k_bias(const void* W, const void* x, const float* bias, float* y,
+                        int M, int K, hipStream_t stream);
+
 /* Replaces residual_add, src/kernels/ops.cuh:265-270: x[i] += residual[i]. */
 int fence_residual_add(float* x, const float* residual, int n, hipStream_t stream);
 

@@ -14,6 +14,7 @@
 #define FENCE_OPS_HPP
 
 #include "fence/ops.h"
+#include "fence/q6k_types.h"
 #include "fence/q8_0_types.h"
 
 namespace fence_detail {
@@ -72,6 +73,18 @@ inline void embed_q8_0(float* d_out, const block_q8_0* d_weight, int token_id, i
 inline void gemv_q8_0(const block_q8_0* d_W, const float* d_x, float* d_y, int M, int K,
                       hipStream_t stream = 0) {
     fence_detail::record(fence_gemv_q8_0(d_W, d_x, d_y, M, K, stream));
+}
+
+/* src/kernels/gemv_q6k.cuh:89 */
+inline void gemv_q6k(const block_q6_K* d_W, const __half* d_x, float* d_y, int M, int K,
+                     hipStream_t stream = 0) {
+    fence_detail::record(fence_gemv_q6k(d_W, d_x, d_y, M, K, stream));
+}
+
+/* src/kernels/gemv_q6k.cuh:140 */
+inline void gemv_q6k_bias(const block_q6_K* d_W, const __half* d_x, const float* d_bias, float* d_y,
+                          int M, int K, hipStream_t stream = 0) {
+    fence_detail::record(fence_gemv_q6k_bias(d_W, d_x, d_bias, d_y, M, K, stream));
 }
 
 /* src/kernels/ops.cuh:265 */

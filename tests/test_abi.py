@@ -79,6 +79,10 @@ def _raw(name):
     ("fence_gemv_q8_0", (0x1001, 32, 48, 8, 64, None)),           # W not 2-byte aligned
     ("fence_gemv_q8_0", (16, 32, None, 8, 64, None)),
     ("fence_gemv_q8_0", (16, 32, 48, -1, 64, None)),
+    ("fence_gemv_q6k", (16, 32, 48, 8, 300, None)),               # K % 256 != 0
+    ("fence_gemv_q6k", (0x1001, 32, 48, 8, 256, None)),           # W not 2-byte aligned
+    ("fence_gemv_q6k", (16, 32, 48, 8, 0, None)),                 # K == 0
+    ("fence_gemv_q6k_bias", (16, 32, None, 48, 8, 256, None)),    # bias missing
     ("fence_residual_add", (16, None, 8, None)),
     ("fence_residual_add", (BAD, 32, 8, None)),
     ("fence_f32_to_f16", (0x1001, 32, 8, None)),                  # binary16 output not 2-byte aligned
@@ -101,6 +105,7 @@ def test_zero_sized_calls_are_no_ops(fence):
     assert _raw("fence_embed_q8_0_gather")(16, 32, 10, 48, 0, 64, None) == 0
     assert _raw("fence_gemv_q8_0")(16, 32, 48, 0, 64, None) == 0
     assert _raw("fence_residual_add")(16, 32, 0, None) == 0
+    assert _raw("fence_gemv_q6k")(16, 32, 48, 0, 256, None) == 0
     assert _raw("fence_f32_to_f16")(16, 32, 0, None) == 0
     assert _raw("fence_residual_rms_norm_f16")(16, 32, 48, None, 64, 0, 64, 1e-6, None) == 0
     assert _raw("fence_swiglu_f16")(16, None, 32, 48, 0, None) == 0
