@@ -1,0 +1,452 @@
+// attention.hip -- decode-step attention over the binary16 KV cache, and the
+// KV store and greedy argmax, on gfx950.
+//
+// Follows gqa_attention, src/kernels/ops.cuh:320-413: for query head h (kv
+// head h / (n_q/n_kv)), over the seq_len cached positions t,
+//   s_t = (q_h . k_t) * scale,   p = softmax(s),   out_h = sum_t p_t v_t,
+// with caches laid out [max_ctx][n_kv][head_dim] in binary16 and
+// scale = 1/sqrt(head_dim) (computed on the host, rounded to fp32).  And
+// store_kv, ops.cuh:419-443: k_cache[pos][i] = binary16(k[i]), v likewise.
+//
+// The reference runs one 256-thread block per query head (32 blocks for
+// Qwen3-4B on a 256-CU GPU) and reads each kv head's K and V once per query
+// head of its group.  Here the sequence is split over many workgroups
+// (split-K decoding): a workgroup takes one kv head, GT query heads of its
+// group and one range of positions, so K and V rows are read once for the
+// whole group.  16 lanes per position (8 dims each, one 128-bit load of K and
+// one of V per lane); the q . k dot is reduced with DPP inside the 16-lane
+// row.  With one split the workgroup writes the output; otherwise it writes
+// (m, l, o) per head to the caller's score_buf -- the reference's scratch
+// argument -- and a second kernel merges the splits.  Nothing is allocated.
+#include "common.hpp"
+
+// Workgroups the split-K grid aims for (splits are also capped by score_buf).
+#ifndef FENCE_ATTN_GT_MAX
+#define FENCE_ATTN_GT_MAX 2
+#endif
+#ifndef FENCE_ATTN_TARGET_WG
+#define FENCE_ATTN_TARGET_WG 512
+#endif
+
+namespace fence {
+namespace {
+
+#ifndef FENCE_ATTN_THREADS
+#define FENCE_ATTN_THREADS 256
+#endif
+constexpr int kThreads = FENCE_ATTN_THREADS;  // split kernel workgroup
+#ifndef FENCE_ATTN_PPG
+#define FENCE_ATTN_PPG 4  // positions per 16-lane group per sub-chunk
+#endif
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+// 2^x by the hardware's v_exp_f32.  Scores are kept in log2 units
+// (s * scale * log2 e), so exp(s_t - m) is one instruction -- the form the
+// reference's fast-math expf also takes (2^(x log2 e)).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Split kernel: grid (n_kv * head_groups, splits); HD = 128.  The workgroup
+// walks its positions in sub-chunks of kSub: (A) every 16-lane group scores
+// its positions for the GT heads into LDS, (B) one wave per head takes the
+// sub-chunk's maximum and exponentials (each computed once) and rescales the
+// running sum, (C) every lane accumulates p * v for its 8 dims.  The V rows
+// of a sub-chunk are loaded together with its K rows, before phase A.
+// FINAL: one split, write the output; else write (m, l, o) partials to ws.
+template <int GT, bool FINAL>
+__global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict__ out, float* __restrict__ ws,
+                                                              const float* __restrict__ q,
+                                                              const uint16_t* __restrict__ kc,
+                                                              const uint16_t* __restrict__ vc, int n_q, int n_kv,
+                                                              int seq_len, int chunk, float scale2) {
+    constexpr int HD = 128;
+    constexpr int kPG = kThreads / 16;     // position groups (16 lanes each)
+    constexpr int kPPG = FENCE_ATTN_PPG;   // positions per group per sub-chunk
+    constexpr int kSub = kPG * kPPG;       // positions per sub-chunk
+    __shared__ float sp[GT][kSub];         // scores, then weights p
+    __shared__ float hm[GT], hl[GT], hc[GT];
+    __shared__ __align__(16) float xo[kPG][GT][HD];
+    const int group = n_q / n_kv;
+    const int head_groups = (group + GT - 1) / GT;
+    const int kvh = blockIdx.x / head_groups;
+    const int h0 = kvh * group + (blockIdx.x % head_groups) * GT;  // first query head of this workgroup
+    const int ng = min(GT, kvh * group + group - h0);              // heads present (GT or fewer)
+    const int split = blockIdx.y;
+    const int t_begin = split * chunk;
+    const int t_end = min(seq_len, t_begin + chunk);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int pg = threadIdx.x >> 4;  // position group
+    const int sl = lane & 15;         // dims [8 sl, 8 sl + 8)
+    const int64_t kv_dim = static_cast<int64_t>(n_kv) * HD;
+
+    float qv[GT][8];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        const int h = h0 + (g < ng ? g : 0);  // a missing head repeats head h0 and is not written
+        const f4 a = *reinterpret_cast<const f4*>(q + static_cast<int64_t>(h) * HD + 8 * sl);
+        const f4 b = *reinterpret_cast<const f4*>(q + static_cast<int64_t>(h) * HD + 8 * sl + 4);
+        qv[g][0] = a.x, qv[g][1] = a.y, qv[g][2] = a.z, qv[g][3] = a.w;
+        qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
+    }
+    float o[GT][8];
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
+    if (threadIdx.x < GT) {
+        hm[threadIdx.x] = -__builtin_inff();
+        hl[threadIdx.x] = 0.0f;
+    }
+
+    const uint16_t* kbase = kc + static_cast<int64_t>(kvh) * HD + 8 * sl;
+    const uint16_t* vbase = vc + static_cast<int64_t>(kvh) * HD + 8 * sl;
+    for (int t0 = t_begin; t0 < t_end; t0 += kSub) {
+        h8 kr[kPPG], vr[kPPG];
+        bool on[kPPG];
+#pragma unroll
+        for (int i = 0; i < kPPG; ++i) {  // the sub-chunk's K and V rows, all loads first
+            const int t = t0 + pg + kPG * i;
+            on[i] = t < t_end;
+            const int64_t tc = on[i] ? t : t_begin;  // clamped: a valid cached position
+            kr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(kbase + tc * kv_dim));
+            vr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(vbase + tc * kv_dim));
+        }
+        // (A) scores, in log2 units
+#pragma unroll
+        for (int i = 0; i < kPPG; ++i) {
+            float kf[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) kf[k] = static_cast<float>(kr[i][k]);
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                float d = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) d = __builtin_fmaf(qv[g][k], kf[k], d);
+                d = group_reduce<16>(d, OpAdd{});
+                if (sl == 0) sp[g][pg + kPG * i] = on[i] ? d * scale2 : -__builtin_inff();
+            }
+        }
+        __syncthreads();
+        // (B) one wave per head: the sub-chunk's maximum, weights and sum
+        if (wave < GT) {
+            const int g = wave;
+            float m = -__builtin_inff();
+            for (int t = lane; t < kSub; t += 64) m = fmaxf(m, sp[g][t]);
+            m = wave_reduce(m, OpMax{});
+            const float mo = hm[g];
+            const float mn = fmaxf(mo, m);
+            float l = 0.0f;
+            for (int t = lane; t < kSub; t += 64) {
+                const float p = sp[g][t] == -__builtin_inff() ? 0.0f : exp2_hw(sp[g][t] - mn);
+                sp[g][t] = p;
+                l += p;
+            }
+            l = wave_reduce(l, OpAdd{});
+            if (lane == 0) {
+                const float c = hl[g] == 0.0f ? 0.0f : exp2_hw(mo - mn);  // nothing seen yet: no old weight
+                hl[g] = hl[g] * c + l;
+                hm[g] = mn;
+                hc[g] = c;
+            }
+        }
+        __syncthreads();
+        // (C) o = o * c + sum_t p_t v_t over the lane's dims
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            const float c = hc[g];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[g][k] *= c;
+        }
+#pragma unroll
+        for (int i = 0; i < kPPG; ++i) {
+            float vf[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) vf[k] = static_cast<float>(vr[i][k]);
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                const float p = sp[g][pg + kPG * i];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) o[g][k] = __builtin_fmaf(p, vf[k], o[g][k]);
+            }
+        }
+        __syncthreads();  // sp and hc are rewritten by the next sub-chunk
+    }
+
+    // Sum the position groups' outputs (they share the running maximum).
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        f4 lo, hi;
+        lo.x = o[g][0], lo.y = o[g][1], lo.z = o[g][2], lo.w = o[g][3];
+        hi.x = o[g][4], hi.y = o[g][5], hi.z = o[g][6], hi.w = o[g][7];
+        *reinterpret_cast<f4*>(&xo[pg][g][8 * sl]) = lo;
+        *reinterpret_cast<f4*>(&xo[pg][g][8 * sl + 4]) = hi;
+    }
+    __syncthreads();
+    // thread (g, d): one output element of one head
+    for (int e = threadIdx.x; e < GT * HD; e += kThreads) {
+        const int g = e / HD, d = e % HD;
+        if (g >= ng) continue;
+        float acc = 0.0f;
+        for (int k = 0; k < kPG; ++k) acc += xo[k][g][d];
+        const float l = hl[g];
+        const int h = h0 + g;
+        if constexpr (FINAL) {
+            out[static_cast<int64_t>(h) * HD + d] = l == 0.0f ? 0.0f : acc / l;
+        } else {
+            // partial of (head h, split): [m, l, o[HD]]
+            float* p = ws + (static_cast<int64_t>(h) * gridDim.y + split) * (HD + 2);
+            if (d == 0) {
+                p[0] = hm[g];
+                p[1] = l;
+            }
+            p[2 + d] = acc;
+        }
+    }
+}
+
+// Merge kernel: one workgroup of HD threads per query head.  The splits'
+// (m, l) go through LDS with one weight c_s = 2^(m_s - M) each, then every
+// thread sums c_s * o_s[d] with its loads issued eight at a time.
+constexpr int kMaxMergeSplits = 1024;
+
+__global__ __launch_bounds__(128) void attn_merge_kernel(float* __restrict__ out, const float* __restrict__ ws,
+                                                         int splits) {
+    constexpr int HD = 128;
+    __shared__ float cw[kMaxMergeSplits];
+    __shared__ float red[2];
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float* p = ws + static_cast<int64_t>(h) * splits * (HD + 2);
+    float m = -__builtin_inff();
+    for (int s = d; s < splits; s += HD) m = fmaxf(m, p[s * (HD + 2)]);
+    m = block_reduce<2>(m, OpMax{}, red);
+    __syncthreads();
+    float l = 0.0f;
+    for (int s = d; s < splits; s += HD) {
+        const float ls = p[s * (HD + 2) + 1];
+        const float c = ls == 0.0f ? 0.0f : exp2_hw(p[s * (HD + 2)] - m);  // an empty split weighs 0
+        cw[s] = c;
+        l += ls * c;
+    }
+    l = block_reduce<2>(l, OpAdd{}, red);  // its barrier also publishes cw[]
+    float o = 0.0f;
+    constexpr int kBatch = 8;
+    for (int s0 = 0; s0 < splits; s0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int s = s0 + b < splits ? s0 + b : s0;  // clamped: a valid split
+            v[b] = p[s * (HD + 2) + 2 + d];
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+            if (s0 + b < splits) o = __builtin_fmaf(cw[s0 + b], v[b], o);
+    }
+    out[static_cast<int64_t>(h) * HD + d] = l == 0.0f ? 0.0f : o / l;
+}
+
+// Any head_dim / alignment: one workgroup per query head, the reference's
+// three passes with the scores kept in ws (n_q x max_ctx, as the reference).
+__global__ __launch_bounds__(256) void attn_generic_kernel(float* __restrict__ out, float* __restrict__ ws,
+                                                           const float* __restrict__ q,
+                                                           const uint16_t* __restrict__ kc,
+                                                           const uint16_t* __restrict__ vc, int hd, int n_q,
+                                                           int n_kv, int seq_len, int max_ctx, float scale) {
+    __shared__ float red[4];
+    const int h = blockIdx.x;
+    const int kvh = h / (n_q / n_kv);
+    const int64_t kv_dim = static_cast<int64_t>(n_kv) * hd;
+    float* s = ws + static_cast<int64_t>(h) * max_ctx;
+    const float* qh = q + static_cast<int64_t>(h) * hd;
+    for (int t = threadIdx.x; t < seq_len; t += 256) {
+        const uint16_t* k = kc + t * kv_dim + static_cast<int64_t>(kvh) * hd;
+        float dot = 0.0f;
+        for (int d = 0; d < hd; ++d) dot = __builtin_fmaf(qh[d], static_cast<float>(__builtin_bit_cast(_Float16, k[d])), dot);
+        s[t] = dot * scale;
+    }
+    float mx = -1e30f;
+    for (int t = threadIdx.x; t < seq_len; t += 256) mx = fmaxf(mx, s[t]);
+    mx = block_reduce<4>(mx, OpMax{}, red);
+    __syncthreads();
+    float sum = 0.0f;
+    for (int t = threadIdx.x; t < seq_len; t += 256) {
+        const float e = expf(s[t] - mx);
+        s[t] = e;
+        sum += e;
+    }
+    sum = block_reduce<4>(sum, OpAdd{}, red);
+    const float inv = 1.0f / sum;
+    __syncthreads();  // every s[t] written above is visible below
+    for (int d = threadIdx.x; d < hd; d += 256) {
+        float acc = 0.0f;
+        for (int t = 0; t < seq_len; ++t)
+            acc = __builtin_fmaf(s[t] * inv,
+                                 static_cast<float>(__builtin_bit_cast(
+                                     _Float16, vc[t * kv_dim + static_cast<int64_t>(kvh) * hd + d])),
+                                 acc);
+        out[static_cast<int64_t>(h) * hd + d] = seq_len > 0 ? acc : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void store_kv_kernel(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                       const float* __restrict__ k, const float* __restrict__ v,
+                                                       int64_t row, int kv_dim, int vec) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (vec) {
+        if (4 * i >= kv_dim) return;
+        st_h4<false>(kc + row + 4 * i, *reinterpret_cast<const f4*>(k + 4 * i));
+        st_h4<false>(vc + row + 4 * i, *reinterpret_cast<const f4*>(v + 4 * i));
+    } else if (i < kv_dim) {
+        kc[row + i] = f32_to_f16_bits(k[i]);
+        vc[row + i] = f32_to_f16_bits(v[i]);
+    }
+}
+
+// argmax (greedy sampling): one workgroup of 1024 threads, float4 loads when
+// aligned; each thread keeps the first index of its largest value, and the
+// tree keeps the larger value, or the lower index on a tie.
+__global__ __launch_bounds__(1024) void argmax_kernel(int* __restrict__ result, const float* __restrict__ x, int n,
+                                                      int vec) {
+    __shared__ float bv[1024];
+    __shared__ int bi[1024];
+    float best = -1e30f;
+    int idx = 0;
+    if (vec) {
+        const int n4 = n >> 2;
+        constexpr int kBatch = 8;  // float4 loads a thread has in flight
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 1024 * kBatch) {
+            f4 v[kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int i = i0 + 1024 * b;
+                v[b] = ld4<true>(x + 4 * (i < n4 ? i : i0));  // clamped: inside x
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {  // in index order, so a tie keeps the first
+                const int i = i0 + 1024 * b;
+                if (i < n4) {
+                    if (v[b].x > best) best = v[b].x, idx = 4 * i;
+                    if (v[b].y > best) best = v[b].y, idx = 4 * i + 1;
+                    if (v[b].z > best) best = v[b].z, idx = 4 * i + 2;
+                    if (v[b].w > best) best = v[b].w, idx = 4 * i + 3;
+                }
+            }
+        }
+        for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024)
+            if (x[i] > best) best = x[i], idx = i;
+    } else {
+        for (int i = threadIdx.x; i < n; i += 1024)
+            if (x[i] > best) best = x[i], idx = i;
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (unsigned s = 512; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            const float ov = bv[threadIdx.x + s];
+            const int oi = bi[threadIdx.x + s];
+            if (ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
+                bv[threadIdx.x] = ov;
+                bi[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *result = bi[0];
+}
+
+template <int GT>
+int launch_split(float* out, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc, int n_q, int n_kv,
+                 int seq_len, int64_t ws_floats, float scale, hipStream_t s) {
+    constexpr int HD = 128;
+    const int group = n_q / n_kv;
+    const int head_groups = (group + GT - 1) / GT;
+    const int base_wg = n_kv * head_groups;
+    // splits: enough workgroups to fill the GPU, at least 64 positions each,
+    // and no more partials than score_buf holds
+    int64_t splits = (FENCE_ATTN_TARGET_WG + base_wg - 1) / base_wg;
+    const int64_t by_len = (seq_len + 63) / 64;
+    if (splits > by_len) splits = by_len;
+    const int64_t by_ws = ws ? ws_floats / (static_cast<int64_t>(n_q) * (HD + 2)) : 1;
+    if (splits > by_ws) splits = by_ws;
+    if (splits < 1) splits = 1;
+    if (splits > kMaxMergeSplits) splits = kMaxMergeSplits;
+    const int chunk = static_cast<int>((seq_len + splits - 1) / splits);
+    const dim3 grid(static_cast<unsigned>(base_wg), static_cast<unsigned>(splits));
+    if (splits == 1)
+        return launch(attn_split_kernel<GT, true>, grid, dim3(kThreads), 0, s, out, ws, q, kc, vc, n_q, n_kv, seq_len,
+                      chunk, scale);
+    if (int st = launch(attn_split_kernel<GT, false>, grid, dim3(kThreads), 0, s, out, ws, q, kc, vc, n_q, n_kv,
+                        seq_len, chunk, scale))
+        return st;
+    return launch(attn_merge_kernel, dim3(static_cast<unsigned>(n_q)), dim3(HD), 0, s, out, ws,
+                  static_cast<int>(splits));
+}
+
+}  // namespace
+
+int gqa_attention_launch(float* out, const float* q, const void* kcv, const void* vcv, int hd, int n_q, int n_kv,
+                         int seq_len, int max_ctx, float* ws, hipStream_t s) {
+    if (!out || !q || !kcv || !vcv || hd <= 0 || n_q <= 0 || n_kv <= 0 || (n_q % n_kv) != 0)
+        return FENCE_ERROR_INVALID_VALUE;
+    if (seq_len < 0 || max_ctx < 1 || seq_len > max_ctx) return FENCE_ERROR_INVALID_VALUE;
+    const uint16_t* kc = static_cast<const uint16_t*>(kcv);
+    const uint16_t* vc = static_cast<const uint16_t*>(vcv);
+    if (!aligned(out, 4) || !aligned(q, 4) || !aligned(kc, 2) || !aligned(vc, 2) || (ws && !aligned(ws, 4)))
+        return FENCE_ERROR_INVALID_VALUE;
+    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+    const float scale2 = scale * 1.44269504088896340736f;  // scores in log2 units for exp2
+    const int64_t ws_floats = static_cast<int64_t>(n_q) * max_ctx;  // the reference's score_buf size
+    const int group = n_q / n_kv;
+    const bool vec = hd == 128 && aligned(q, 16) && aligned(kc, 16) && aligned(vc, 16);
+    if (vec) {
+        if (FENCE_ATTN_GT_MAX == 1) return launch_split<1>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (FENCE_ATTN_GT_MAX == 2 && group >= 2)
+            return launch_split<2>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (group >= 4) return launch_split<4>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (group == 2) return launch_split<2>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (group == 1) return launch_split<1>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        return launch_split<4>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);  // group 3: masked
+    }
+    if (!ws) return FENCE_ERROR_INVALID_VALUE;  // the generic path keeps scores in score_buf
+    return launch(attn_generic_kernel, dim3(static_cast<unsigned>(n_q)), dim3(256), 0, s, out, ws, q, kc, vc, hd,
+                  n_q, n_kv, seq_len, max_ctx, scale);
+}
+
+int store_kv_launch(void* kcv, void* vcv, const float* k, const float* v, int pos, int kv_dim, int max_ctx,
+                    hipStream_t s) {
+    if (!kcv || !vcv || !k || !v || kv_dim < 0 || max_ctx < 1 || pos < 0 || pos >= max_ctx)
+        return FENCE_ERROR_INVALID_VALUE;
+    uint16_t* kc = static_cast<uint16_t*>(kcv);
+    uint16_t* vc = static_cast<uint16_t*>(vcv);
+    if (!aligned(kc, 2) || !aligned(vc, 2) || !aligned(k, 4) || !aligned(v, 4)) return FENCE_ERROR_INVALID_VALUE;
+    if (kv_dim == 0) return FENCE_SUCCESS;
+    const int64_t row = static_cast<int64_t>(pos) * kv_dim;
+    const int vec = (kv_dim % 4 == 0) && aligned(kc + row, 8) && aligned(vc + row, 8) && aligned(k, 16) &&
+                    aligned(v, 16);
+    const int items = vec ? kv_dim / 4 : kv_dim;
+    return launch(store_kv_kernel, dim3(grid_1d(items, 256)), dim3(256), 0, s, kc, vc, k, v, row, kv_dim, vec);
+}
+
+int argmax_launch(const float* x, int* result, int n, hipStream_t s) {
+    if (!x || !result || n < 0 || !aligned(x, 4) || !aligned(result, 4)) return FENCE_ERROR_INVALID_VALUE;
+    return launch(argmax_kernel, dim3(1), dim3(1024), 0, s, result, x, n, aligned(x, 16) ? 1 : 0);
+}
+
+}  // namespace fence
+
+extern "C" int fence_argmax(const float* x, int* result, int n, hipStream_t stream) {
+    return fence::argmax_launch(x, result, n, stream);
+}
+
+extern "C" int fence_gqa_attention(float* attn_out, const float* q, const void* k_cache, const void* v_cache,
+                                   int head_dim, int n_q_heads, int n_kv_heads, int seq_len, int max_ctx,
+                                   float* score_buf, hipStream_t stream) {
+    return fence::gqa_attention_launch(attn_out, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, seq_len,
+                                       max_ctx, score_buf, stream);
+}
+
+extern "C" int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v, int pos, int kv_dim,
+                              int max_ctx, hipStream_t stream) {
+    return fence::store_kv_launch(k_cache, v_cache, k, v, pos, kv_dim, max_ctx, stream);
+}

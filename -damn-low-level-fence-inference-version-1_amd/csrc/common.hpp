@@ -159,9 +159,12 @@ inline int hip_status(hipError_t e) {
 
 // One-shot start/stop events for the next launch on this host thread
 // (fence_time_next_launch).
+// Events for the next `count` launches on this thread: `start` at the first
+// one's kernel start, `stop` at the last one's kernel end.
 struct TimingHook {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
+    int count = 0;
 };
 inline TimingHook& timing_hook() {
     thread_local TimingHook hook;
@@ -173,9 +176,11 @@ inline int launch_impl(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t s
                        hipStream_t stream, Tuple& args, std::index_sequence<I...>) {
     void* ptrs[] = {static_cast<void*>(&std::get<I>(args))..., nullptr};
     TimingHook& hook = timing_hook();
-    if (hook.start || hook.stop) {
-        const hipEvent_t a = hook.start, b = hook.stop;
-        hook = TimingHook{};
+    if (hook.count > 0) {
+        const hipEvent_t a = hook.start;
+        const hipEvent_t b = hook.count == 1 ? hook.stop : nullptr;
+        hook.start = nullptr;
+        if (--hook.count == 0) hook = TimingHook{};
         return hip_status(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block,
                                              ptrs, shmem, stream, a, b, 0));
     }

@@ -12,6 +12,12 @@ extern "C" const char* fence_status_string(int status) {
 extern "C" const char* fence_version(void) { return "fence-mi355x 0.1.0 (gfx950)"; }
 
 extern "C" int fence_time_next_launch(hipEvent_t start, hipEvent_t stop) {
-    fence::timing_hook() = fence::TimingHook{start, stop};
+    fence::timing_hook() = fence::TimingHook{start, stop, 1};
+    return FENCE_SUCCESS;
+}
+
+extern "C" int fence_time_next_launches(hipEvent_t start, hipEvent_t stop, int count) {
+    if (count < 1) return FENCE_ERROR_INVALID_VALUE;
+    fence::timing_hook() = fence::TimingHook{start, stop, count};
     return FENCE_SUCCESS;
 }

@@ -40,6 +40,9 @@ SIGNATURES = {
     "fence_gemv_q8_0": (_P, _P, _P, _I, _I, _P),
     "fence_gemv_q6k": (_P, _P, _P, _I, _I, _P),
     "fence_gemv_q6k_bias": (_P, _P, _P, _P, _I, _I, _P),
+    "fence_gqa_attention": (_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P),
+    "fence_store_kv": (_P, _P, _P, _P, _I, _I, _I, _P),
+    "fence_argmax": (_P, _P, _I, _P),
     "fence_residual_add": (_P, _P, _I, _P),
     "fence_f32_to_f16": (_P, _P, _I, _P),
     "fence_f16_to_f32": (_P, _P, _I, _P),
@@ -56,6 +59,7 @@ SIGNATURES = {
     "fence_embed_q8_0_gather_rms_norm": (_P, _P, _L, _P, _L, _I, _P, _F, _P),
     "fence_rope_inv_freq": (_P, _I, _F),
     "fence_time_next_launch": (_P, _P),
+    "fence_time_next_launches": (_P, _P, _I),
     "fence_status_string": (_I,),
     "fence_version": (),
 }
@@ -152,6 +156,20 @@ def gemv_q6k_bias(W, x, bias, y, M, K, stream=None):
     _call("fence_gemv_q6k_bias", W, x, bias, y, M, K, stream)
 
 
+def gqa_attention(attn_out, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, seq_len, max_ctx,
+                  score_buf, stream=None):
+    _call("fence_gqa_attention", attn_out, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads,
+          seq_len, max_ctx, score_buf, stream)
+
+
+def store_kv(k_cache, v_cache, k, v, pos, kv_dim, max_ctx, stream=None):
+    _call("fence_store_kv", k_cache, v_cache, k, v, pos, kv_dim, max_ctx, stream)
+
+
+def argmax(x, result, n, stream=None):
+    _call("fence_argmax", x, result, n, stream)
+
+
 def residual_add(x, residual, n, stream=None):
     _call("fence_residual_add", x, residual, n, stream)
 
@@ -218,6 +236,12 @@ def time_next_launch(start, stop) -> None:
     """Record hipEvent handles `start`/`stop` around the next kernel this
     thread launches (kernel execution interval only)."""
     _call("fence_time_next_launch", start, stop)
+
+
+def time_next_launches(start, stop, count) -> None:
+    """Hook the next `count` launches: start at the first kernel's start,
+    stop at the last one's end."""
+    _call("fence_time_next_launches", start, stop, count)
 
 
 def rope_inv_freq(head_dim: int, freq_base: float):

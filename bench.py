@@ -480,7 +480,9 @@ def all_configs(torch, F, path, reps):
 
     scrub = {"buf": None}
 
-    def measure(cfg, name, nbytes, make_set, run, note=""):
+    def measure(cfg, name, nbytes, make_set, run, note="", launches=1):
+        """launches: kernels the call runs; the timing spans the first one's
+        start to the last one's end."""
         probe = make_set()
         sb = sum(t.numel() * t.element_size() for t in probe.values() if torch.is_tensor(t))
         small = sb < (16 << 20)
@@ -493,13 +495,14 @@ def all_configs(torch, F, path, reps):
         for i in range(reps):
             if small:  # untimed 1 GiB write evicts the small inputs from every cache level
                 scrub["buf"].zero_()
-            F.time_next_launch(*evs[i])
+            F.time_next_launches(*evs[i], launches)
             run(sets[i % len(sets)])
         torch.cuda.synchronize()
         ts = sorted(hev.elapsed_ms(a, b) * 1e3 for a, b in evs)
         mean = sum(ts) / len(ts)
         gbps = nbytes / (mean * 1e-6) / 1e9
         r = {"config": cfg, "op": name, "bytes": int(nbytes), "us_mean": round(mean, 3),
+             "launches": launches,
              "us_p10": round(ts[len(ts) // 10], 3), "us_p50": round(ts[len(ts) // 2], 3),
              "us_p90": round(ts[(9 * len(ts)) // 10], 3), "GBps": round(gbps, 1),
              "frac_peak": round(gbps / PEAK_HBM_GBPS, 4), "sets": len(sets),
@@ -561,6 +564,24 @@ def all_configs(torch, F, path, reps):
                                           y=torch.empty(pm, **dev)),
                 lambda b, pm=pm, pk=pk: F.gemv_q6k(b["W"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(),
                                                    pm, pk, sh))
+    # decode attention over the binary16 KV cache (qwen3.cu:302-305), Qwen3-4B heads, max_ctx 4096
+    for seqa in (256, 1024, 2915, 4096):
+        measure(0, f"gqa_attention 32q/8kv x128 seq {seqa} (+merge)", seqa * 1024 * 2 * 2 + 4096 * 8,
+                lambda: dict(kc=randn(4096, 1024).half(), vc=randn(4096, 1024).half(), q=randn(4096) * 0.3,
+                             o=torch.empty(4096, **dev), ws=torch.empty(32 * 4096, **dev)),
+                lambda b, seqa=seqa: F.gqa_attention(b["o"].data_ptr(), b["q"].data_ptr(), b["kc"].data_ptr(),
+                                                     b["vc"].data_ptr(), 128, 32, 8, seqa, 4096,
+                                                     b["ws"].data_ptr(), sh),
+                launches=1 if seqa <= 64 else 2)
+    measure(0, "store_kv 8x128 (one position)", 1024 * (4 + 2) * 2,
+            lambda: dict(kc=torch.empty(4096, 1024, dtype=torch.float16, device="cuda"),
+                         vc=torch.empty(4096, 1024, dtype=torch.float16, device="cuda"),
+                         k=randn(1024), v=randn(1024)),
+            lambda b: F.store_kv(b["kc"].data_ptr(), b["vc"].data_ptr(), b["k"].data_ptr(), b["v"].data_ptr(),
+                                 2915, 1024, 4096, sh))
+    measure(0, f"argmax {V0}", V0 * 4 + 4,
+            lambda: dict(x=randn(V0), r=torch.empty(1, dtype=torch.int32, device="cuda")),
+            lambda b: F.argmax(b["x"].data_ptr(), b["r"].data_ptr(), V0, sh))
     # tied LM head (qwen3.cu:261): the whole table is read once per decoded token
     measure(0, f"gemv_q8_0 lm head {V0}x{E0}", gemv_bytes(V0, E0),
             lambda: dict(t=make_q8_0_table(torch, gen, V0, E0), x=randn(E0), y=torch.empty(V0, **dev)),

@@ -119,6 +119,31 @@ int fence_gemv_q6k(const void* W, const void* x, float* y, int M, int K,
 int fence_gemv_q6k_bias(const void* W, const void* x, const float* bias, float* y,
                         int M, int K, hipStream_t stream);
 
+/* Replaces gqa_attention, src/kernels/ops.cuh:320-413 (src/model/qwen3.cu:
+ * 304-305): attention of one query position over the seq_len cached
+ * positions.  q [n_q_heads][head_dim] fp32; caches [max_ctx][n_kv_heads]
+ * [head_dim] binary16; attn_out [n_q_heads][head_dim] fp32.  score_buf holds
+ * n_q_heads * max_ctx floats, as in the reference; it is used as scratch
+ * (split-sequence partials) and its contents afterwards are unspecified.
+ * scale = 1/sqrt(head_dim) in fp32.  seq_len 0 writes zeros; seq_len >
+ * max_ctx or n_q_heads % n_kv_heads != 0 is FENCE_ERROR_INVALID_VALUE.  Calls
+ * that share a score_buf must not overlap. */
+int fence_gqa_attention(float* attn_out, const float* q, const void* k_cache,
+                        const void* v_cache, int head_dim, int n_q_heads,
+                        int n_kv_heads, int seq_len, int max_ctx, float* score_buf,
+                        hipStream_t stream);
+
+/* Replaces store_kv, src/kernels/ops.cuh:434-443 (src/model/qwen3.cu:302):
+ * k_cache[pos][i] = binary16(k[i]), v_cache[pos][i] = binary16(v[i]), i <
+ * kv_dim.  pos outside [0, max_ctx) is FENCE_ERROR_INVALID_VALUE. */
+int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v,
+                   int pos, int kv_dim, int max_ctx, hipStream_t stream);
+
+/* Replaces argmax, src/kernels/ops.cuh:482-487 (greedy sampling):
+ * *result = index of the largest of x[0..n), the lowest such index on a tie;
+ * NaN never wins; n == 0 gives 0. */
+int fence_argmax(const float* x, int* result, int n, hipStream_t stream);
+
 /* Replaces residual_add, src/kernels/ops.cuh:265-270: x[i] += residual[i]. */
 int fence_residual_add(float* x, const float* residual, int n, hipStream_t stream);
 
@@ -233,6 +258,11 @@ int fence_rope_inv_freq(float* inv_freq, int head_dim, float freq_base);
  * No counterpart in the reference (it has no timing facility); used by the
  * benchmark. */
 int fence_time_next_launch(hipEvent_t start, hipEvent_t stop);
+
+/* The same over the next `count` launches of this thread (an entry point
+ * that launches several kernels): start at the first kernel's start, stop at
+ * the last one's end.  count < 1 is FENCE_ERROR_INVALID_VALUE. */
+int fence_time_next_launches(hipEvent_t start, hipEvent_t stop, int count);
 
 /* Static text for a status code. */
 const char* fence_status_string(int status);

@@ -87,6 +87,25 @@ inline void gemv_q6k_bias(const block_q6_K* d_W, const __half* d_x, const float*
     fence_detail::record(fence_gemv_q6k_bias(d_W, d_x, d_bias, d_y, M, K, stream));
 }
 
+/* src/kernels/ops.cuh:405 */
+inline void gqa_attention(float* attn_out, const float* q, const half* k_cache, const half* v_cache,
+                          int head_dim, int n_q_heads, int n_kv_heads, int seq_len, int max_ctx,
+                          float* score_buf, hipStream_t stream = 0) {
+    fence_detail::record(fence_gqa_attention(attn_out, q, k_cache, v_cache, head_dim, n_q_heads,
+                                             n_kv_heads, seq_len, max_ctx, score_buf, stream));
+}
+
+/* src/kernels/ops.cuh:434 */
+inline void store_kv(half* k_cache, half* v_cache, const float* k, const float* v, int pos,
+                     int kv_dim, int max_ctx, hipStream_t stream = 0) {
+    fence_detail::record(fence_store_kv(k_cache, v_cache, k, v, pos, kv_dim, max_ctx, stream));
+}
+
+/* src/kernels/ops.cuh:482 */
+inline void argmax(const float* x, int* result, int n, hipStream_t stream = 0) {
+    fence_detail::record(fence_argmax(x, result, n, stream));
+}
+
 /* src/kernels/ops.cuh:265 */
 inline void residual_add(float* x, const float* residual, int n, hipStream_t stream = 0) {
     fence_detail::record(fence_residual_add(x, residual, n, stream));

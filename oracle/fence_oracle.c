@@ -8,6 +8,7 @@
 #include "fence_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 static float bits_to_f32(uint32_t b) {
@@ -351,6 +352,59 @@ void fo_swiglu_f16(uint16_t* out16, float* out, const float* gate, const float* 
         if (out) out[i] = v;
         out16[i] = fo_f32_to_f16(v);
     }
+}
+
+/* ------------------------------------------------- decode attention, KV */
+
+/* src/kernels/ops.cuh:419-432 */
+void fo_store_kv(uint16_t* k_cache, uint16_t* v_cache, const float* k, const float* v,
+                 int pos, int kv_dim) {
+    for (int i = 0; i < kv_dim; ++i) {
+        k_cache[(int64_t)pos * kv_dim + i] = fo_f32_to_f16(k[i]);
+        v_cache[(int64_t)pos * kv_dim + i] = fo_f32_to_f16(v[i]);
+    }
+}
+
+/* src/kernels/ops.cuh:320-404 */
+void fo_gqa_attention(float* out, const float* q, const uint16_t* k_cache,
+                      const uint16_t* v_cache, int head_dim, int n_q_heads,
+                      int n_kv_heads, int seq_len, int max_ctx) {
+    (void)max_ctx;
+    const int group = n_q_heads / n_kv_heads;
+    const int64_t kv_dim = (int64_t)n_kv_heads * head_dim;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float s_small[1];
+    float* s = seq_len > 0 ? (float*)malloc(sizeof(float) * (size_t)seq_len) : s_small;
+    for (int h = 0; h < n_q_heads; ++h) {
+        const int kvh = h / group;
+        const float* qh = q + (int64_t)h * head_dim;
+        for (int t = 0; t < seq_len; ++t) {
+            const uint16_t* kt = k_cache + t * kv_dim + (int64_t)kvh * head_dim;
+            double dot = 0.0;
+            for (int d = 0; d < head_dim; ++d) dot += (double)qh[d] * (double)fo_fp16_to_f32(kt[d]);
+            s[t] = (float)dot * scale;
+        }
+        softmax_row(s, seq_len);
+        for (int d = 0; d < head_dim; ++d) {
+            double acc = 0.0;
+            for (int t = 0; t < seq_len; ++t)
+                acc += (double)s[t] * (double)fo_fp16_to_f32(v_cache[t * kv_dim + (int64_t)kvh * head_dim + d]);
+            out[(int64_t)h * head_dim + d] = (float)acc;
+        }
+    }
+    if (s != s_small) free(s);
+}
+
+/* src/kernels/ops.cuh:448-480: the largest value; ties go to the lowest index */
+int fo_argmax(const float* x, int n) {
+    float best = -1e30f;
+    int idx = 0;
+    for (int i = 0; i < n; ++i)
+        if (x[i] > best) {
+            best = x[i];
+            idx = i;
+        }
+    return idx;
 }
 
 /* ------------------------------------------------------ fused compositions */

@@ -117,6 +117,24 @@ double fo_q6k_dot(const uint8_t* blk, const uint16_t* x16);
 void fo_gemv_q6k(const uint8_t* W, const uint16_t* x16, const float* bias, float* y,
                  int M, int K);
 
+/* store_kv, src/kernels/ops.cuh:419-443: k_cache[pos*kv_dim + i] =
+ * binary16(k[i]), the same for v (caches are binary16 bit patterns). */
+void fo_store_kv(uint16_t* k_cache, uint16_t* v_cache, const float* k, const float* v,
+                 int pos, int kv_dim);
+/* gqa_attention, src/kernels/ops.cuh:320-413, one query position: for query
+ * head h (kv head h / (n_q/n_kv)), s_t = (q_h . k_t) * scale over the
+ * seq_len cached positions, p = softmax(s) (the -1e30 initial maximum and
+ * e * (1/sum) of the reference), out_h = sum_t p_t v_t.  Caches are
+ * [max_ctx][n_kv][head_dim] binary16; scale = 1/sqrt(head_dim) rounded to
+ * fp32.  Dots and the output sum accumulate in double. */
+void fo_gqa_attention(float* out, const float* q, const uint16_t* k_cache,
+                      const uint16_t* v_cache, int head_dim, int n_q_heads,
+                      int n_kv_heads, int seq_len, int max_ctx);
+/* argmax, src/kernels/ops.cuh:448-487 reduced: the first index of the
+ * maximum (the reference keeps the first index among a thread's strided
+ * elements and the larger value across threads); -1e30 initial maximum. */
+int fo_argmax(const float* x, int n);
+
 /* IEEE binary32 -> binary16, round to nearest, ties to even; overflow -> inf;
  * NaN -> quiet NaN of the same sign.  The reference's __float2half in
  * f32_to_f16 (src/kernels/ops.cuh:448-462) and float_to_half (:274-289). */

@@ -530,8 +530,72 @@ def check_q6k(o: Oracle):
     return fails
 
 
+# ------------------------------------------------------- decode attention
+
+def attention_ref64(q, kc, vc, n_q, n_kv, hd, seq):
+    """float64 softmax(q k^T / sqrt(hd)) v per query head, from binary16 caches."""
+    K = kc[:seq].view(np.float16).astype(np.float64).reshape(seq, n_kv, hd)
+    V = vc[:seq].view(np.float16).astype(np.float64).reshape(seq, n_kv, hd)
+    qh = np.asarray(q, np.float64).reshape(n_q, hd)
+    out = np.empty((n_q, hd))
+    for h in range(n_q):
+        g = h // (n_q // n_kv)
+        s = K[:, g, :] @ qh[h] / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ V[:, g, :]
+    return out.reshape(-1)
+
+
+def check_attention(o: Oracle):
+    fails = []
+    rng = np.random.default_rng(53)
+    n_q, n_kv, hd, ctx = 8, 2, 64, 40
+    kc = rng.standard_normal((ctx, n_kv * hd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((ctx, n_kv * hd)).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(n_q * hd).astype(np.float32)
+    for seq in (1, 2, 17, 40):
+        got = o.gqa_attention(q, kc, vc, n_q, n_kv, hd, seq)
+        ref = attention_ref64(q, kc, vc, n_q, n_kv, hd, seq)
+        if not np.allclose(got, ref, rtol=1e-5, atol=1e-6):
+            fails.append(f"attention seq={seq}: differs from float64 softmax(qK/sqrt(d))V")
+    # one position: the output is that position's V row, exactly
+    got = o.gqa_attention(q, kc, vc, n_q, n_kv, hd, 1).reshape(n_q, hd)
+    v0 = vc[0].view(np.float16).astype(np.float32).reshape(n_kv, hd)
+    if not np.array_equal(got, v0[np.arange(n_q) // (n_q // n_kv)]):
+        fails.append("attention over one position is not V[0] of the head's kv group")
+    # q = 0: uniform weights, the mean of V
+    got = o.gqa_attention(np.zeros_like(q), kc, vc, n_q, n_kv, hd, 40).reshape(n_q, hd)
+    mean = vc[:40].view(np.float16).astype(np.float64).reshape(40, n_kv, hd).mean(axis=0)
+    if not np.allclose(got, mean[np.arange(n_q) // (n_q // n_kv)], rtol=1e-6, atol=1e-7):
+        fails.append("attention with q = 0 is not the mean of V")
+    # scores far apart: the softmax must subtract the maximum (no overflow)
+    big = (q * 400).astype(np.float32)
+    got = o.gqa_attention(big, kc, vc, n_q, n_kv, hd, 40)
+    if not np.all(np.isfinite(got)) or not np.allclose(got, attention_ref64(big, kc, vc, n_q, n_kv, hd, 40),
+                                                       rtol=1e-5, atol=1e-5):
+        fails.append("attention with large scores overflows or differs")
+    # store_kv writes binary16 of k and v at row pos, nothing else
+    k, v = rng.standard_normal(n_kv * hd).astype(np.float32), rng.standard_normal(n_kv * hd).astype(np.float32)
+    kc2, vc2 = o.store_kv(kc, vc, k, v, 7)
+    ok = (np.array_equal(kc2[7], k.astype(np.float16).view(np.uint16)) and
+          np.array_equal(vc2[7], v.astype(np.float16).view(np.uint16)) and
+          np.array_equal(np.delete(kc2, 7, 0), np.delete(kc, 7, 0)) and
+          np.array_equal(np.delete(vc2, 7, 0), np.delete(vc, 7, 0)))
+    if not ok:
+        fails.append("store_kv: row pos is not binary16(k), binary16(v), or other rows changed")
+    # argmax: first index of the maximum, NaN never wins
+    x = rng.standard_normal(1000).astype(np.float32)
+    x[[10, 700]] = 9.0
+    x[3] = np.nan
+    if o.argmax(x) != 10:
+        fails.append("argmax: not the first index of the maximum")
+    if o.argmax(np.full(5, -np.inf, np.float32)) != 0:
+        fails.append("argmax of all -inf is not 0")
+    return fails
+
+
 ALL_CHECKS = [check_fp16, check_q8_0, check_rms_norm, check_inv_freq, check_rope, check_swiglu,
-              check_softmax, check_fused, check_gemv, check_f16_epilogue, check_q6k]
+              check_softmax, check_fused, check_gemv, check_f16_epilogue, check_q6k, check_attention]
 
 
 def run_all(o: Oracle):

@@ -49,6 +49,9 @@ _SIGS = {
     "fo_q6k_quant": ((_P, _I), ctypes.c_int),
     "fo_q6k_dot": ((_P, _P), ctypes.c_double),
     "fo_gemv_q6k": ((_P, _P, _P, _P, _I, _I), None),
+    "fo_store_kv": ((_P, _P, _P, _P, _I, _I), None),
+    "fo_gqa_attention": ((_P, _P, _P, _P, _I, _I, _I, _I, _I), None),
+    "fo_argmax": ((_P, _I), ctypes.c_int),
     "fo_qk_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
     "fo_rms_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
 }
@@ -214,6 +217,29 @@ class Oracle:
         y = np.empty(M, np.float32)
         self.lib.fo_gemv_q6k(_ptr(w), _ptr(x), _ptr(bz), _ptr(y), M, K)
         return y
+
+    # decode attention ------------------------------------------------------
+    def store_kv(self, k_cache, v_cache, k, v, pos):
+        """Returns updated copies of the binary16 caches [max_ctx, kv_dim]."""
+        kc = np.ascontiguousarray(k_cache, np.uint16).copy()
+        vc = np.ascontiguousarray(v_cache, np.uint16).copy()
+        k, v = _f32(k), _f32(v)
+        self.lib.fo_store_kv(_ptr(kc), _ptr(vc), _ptr(k), _ptr(v), pos, k.size)
+        return kc, vc
+
+    def gqa_attention(self, q, k_cache, v_cache, n_q_heads, n_kv_heads, head_dim, seq_len):
+        """q [n_q*hd] fp32; caches [max_ctx, n_kv*hd] binary16 bits."""
+        q = _f32(q)
+        kc = np.ascontiguousarray(k_cache, np.uint16)
+        vc = np.ascontiguousarray(v_cache, np.uint16)
+        out = np.empty(n_q_heads * head_dim, np.float32)
+        self.lib.fo_gqa_attention(_ptr(out), _ptr(q), _ptr(kc), _ptr(vc), head_dim, n_q_heads, n_kv_heads,
+                                  seq_len, kc.shape[0])
+        return out
+
+    def argmax(self, x):
+        x = _f32(x)
+        return int(self.lib.fo_argmax(_ptr(x), x.size))
 
     # f16 and residual epilogue -------------------------------------------
     def f32_to_f16(self, x):

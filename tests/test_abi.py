@@ -83,6 +83,11 @@ def _raw(name):
     ("fence_gemv_q6k", (0x1001, 32, 48, 8, 256, None)),           # W not 2-byte aligned
     ("fence_gemv_q6k", (16, 32, 48, 8, 0, None)),                 # K == 0
     ("fence_gemv_q6k_bias", (16, 32, None, 48, 8, 256, None)),    # bias missing
+    ("fence_gqa_attention", (16, 32, 48, 64, 128, 6, 4, 10, 100, 80, None)),   # 6 % 4 != 0
+    ("fence_gqa_attention", (16, 32, 48, 64, 128, 8, 2, 101, 100, 80, None)),  # seq_len > max_ctx
+    ("fence_store_kv", (16, 32, 48, 64, 100, 512, 100, None)),                # pos == max_ctx
+    ("fence_store_kv", (16, 32, 48, 64, -1, 512, 100, None)),
+    ("fence_argmax", (16, None, 10, None)),
     ("fence_residual_add", (16, None, 8, None)),
     ("fence_residual_add", (BAD, 32, 8, None)),
     ("fence_f32_to_f16", (0x1001, 32, 8, None)),                  # binary16 output not 2-byte aligned

@@ -48,6 +48,11 @@ MUTANTS = [
     ("q6k_sub_block_32", "(double)scales[i / 16]", "(double)scales[i / 32]"),
     ("q6k_offset_31", "(fo_q6k_quant(blk, i) - 32)", "(fo_q6k_quant(blk, i) - 31)"),
     ("q6k_bias_dropped", "y[r] = bias ? (float)sum + bias[r] : (float)sum;", "y[r] = (float)sum;"),
+    ("attn_group_mapping", "const int kvh = h / group;", "const int kvh = h % n_kv_heads;"),
+    ("attn_scale_1_over_d", "const float scale = 1.0f / sqrtf((float)head_dim);", "const float scale = 1.0f / (float)head_dim;"),
+    ("attn_v_stride", "v_cache[t * kv_dim + (int64_t)kvh * head_dim + d]", "v_cache[t * head_dim + (int64_t)kvh * head_dim + d]"),
+    ("store_kv_wrong_row", "k_cache[(int64_t)pos * kv_dim + i] = fo_f32_to_f16(k[i]);", "k_cache[(int64_t)(pos + 1) * kv_dim + i] = fo_f32_to_f16(k[i]);"),
+    ("argmax_last_tie", "if (x[i] > best) {", "if (x[i] >= best) {"),
     ("qk_norm_k_uses_q_weight", "fo_rms_norm_per_head(k + t * krow, wk,", "fo_rms_norm_per_head(k + t * krow, wq,"),
 ]
 
