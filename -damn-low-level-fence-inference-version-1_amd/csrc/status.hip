@@ -4,6 +4,11 @@
 extern "C" const char* fence_status_string(int status) {
     if (status == FENCE_SUCCESS) return "success";
     if (status == FENCE_ERROR_INVALID_VALUE) return "invalid value (shape, null or misaligned pointer)";
+    if (status == FENCE_ERROR_NOT_FOUND) return "not found";
+    if (status == FENCE_ERROR_OUT_OF_MEMORY) return "out of memory";
+    if (status == FENCE_ERROR_BAD_FILE) return "bad or unreadable GGUF file";
+    if (status == FENCE_ERROR_TYPE_MISMATCH) return "metadata value has another type";
+    if (status == FENCE_ERROR_UNSUPPORTED) return "unsupported model";
     if (status > FENCE_ERROR_HIP_BASE)
         return hipGetErrorString(static_cast<hipError_t>(status - FENCE_ERROR_HIP_BASE));
     return "unknown status";

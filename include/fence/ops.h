@@ -38,6 +38,12 @@ extern "C" {
 enum {
     FENCE_SUCCESS = 0,
     FENCE_ERROR_INVALID_VALUE = 22,
+    /* model files and the host forward (fence/gguf.h, fence/model.h) */
+    FENCE_ERROR_NOT_FOUND = 2,       /* no such tensor or metadata key */
+    FENCE_ERROR_OUT_OF_MEMORY = 12,  /* host or device allocation failed */
+    FENCE_ERROR_BAD_FILE = 74,       /* not a readable, well-formed GGUF file */
+    FENCE_ERROR_TYPE_MISMATCH = 75,  /* metadata value of another type */
+    FENCE_ERROR_UNSUPPORTED = 95,    /* a model this forward does not run */
     FENCE_ERROR_HIP_BASE = 1000
 };
 

@@ -17,8 +17,8 @@ EINVAL = fence_ops.EINVAL
 BAD = 0x1002  # a non-null address that is not 4-byte aligned; never dereferenced
 
 
-def header_declarations():
-    text = open(HEADER).read()
+def header_declarations(path=HEADER):
+    text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
     for m in re.finditer(r"^\s*(?:const\s+)?[\w\s\*]+?\b(fence_\w+)\s*\(([^)]*)\)\s*;", text, re.M):
@@ -38,10 +38,26 @@ def test_header_declares_and_library_exports_everything(fence):
     assert set(fence_ops.SIGNATURES) == set(decls)
 
 
+def test_model_headers_declare_and_library_exports_everything(fence):
+    """include/fence/gguf.h and model.h against the library and fence_model.py."""
+    import fence_model
+    decls = {}
+    for h in ("gguf.h", "model.h"):
+        decls.update(header_declarations(os.path.join(ROOT, "include", "fence", h)))
+    assert len(decls) >= 25
+    lib = fence_model.lib()
+    for name, nargs in decls.items():
+        assert hasattr(lib, name), f"{name} declared but not exported"
+        assert len(fence_model.SIGNATURES[name][0]) == nargs, f"{name}: argument count differs"
+    assert set(fence_model.SIGNATURES) == set(decls)
+
+
 def test_version_and_status_strings(fence):
     assert "gfx950" in fence.version()
     assert fence.status_string(0) == "success"
     assert "invalid" in fence.status_string(EINVAL)
+    for st in (2, 12, 74, 75, 95):  # the loader's and model's statuses
+        assert fence.status_string(st) != "unknown status"
 
 
 def _raw(name):

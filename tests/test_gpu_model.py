@@ -1,0 +1,153 @@
+"""The Qwen3 host forward (include/fence/model.h) on a GPU: a small synthetic
+GGUF model loaded to HBM and decoded token by token, against the oracle's
+forward of the reference's launch sequence (src/model/qwen3.cu:240-341).
+
+Bars:
+  - upload: every tensor's device copy equals the file's bytes;
+  - the fused sequence and the reference's launch sequence give bit-identical
+    logits at every position (the fused kernels round exactly as the unfused
+    chain does);
+  - end to end against the oracle, per position: max|logits - oracle| <=
+    E2E_TOL (4e-3) * max|oracle logits|.  The per-op bars (1e-5 of a row,
+    bit-exact conversions) hold stage by stage (tests/drop_in/decode_step);
+    over a whole forward a binary16 conversion of an activation that lies
+    within an fp32 rounding of a tie can round the other way and carry a
+    2^-11 relative step into the next projection: one-ulp noise on every op
+    moves this model's logits by ~6e-4 of their maximum, a wrong RoPE base by
+    0.2, swapped gate/up weights by 0.9 (tests/test_oracle_forward.py);
+  - greedy tokens equal the oracle's argmax wherever the oracle's top-two
+    margin exceeds that bar.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import fence_model as M
+from fence_ops import EINVAL, FenceError
+from model_files import E2E_TOL, TOKENS, oracle_forward, write_tiny_qwen3
+
+pytestmark = pytest.mark.gpu
+
+CTX = 32
+
+
+def decode(model, tokens, sequence=M.SEQUENCE_FUSED):
+    model.set_sequence(sequence)
+    logits, greedy = [], []
+    for pos, tok in enumerate(tokens):
+        ptr = model.forward(tok, pos)
+        greedy.append(model.sample_greedy(ptr))
+        logits.append(model.logits(ptr))
+    return np.stack(logits), greedy
+
+
+def check_against_oracle(got, greedy, ref):
+    for pos in range(ref.shape[0]):
+        scale = np.max(np.abs(ref[pos]))
+        err = np.max(np.abs(got[pos].astype(np.float64) - ref[pos]))
+        assert err <= E2E_TOL * scale, f"position {pos}: err {err:.3g} > {E2E_TOL:g} * {scale:.3g}"
+        top2 = np.sort(ref[pos])[-2:]
+        if top2[1] - top2[0] > 2 * E2E_TOL * scale:
+            assert greedy[pos] == int(np.argmax(ref[pos])), f"position {pos}: greedy token differs"
+    print(f"worst err / max|logit| = "
+          f"{max(np.max(np.abs(got[p] - ref[p])) / np.max(np.abs(ref[p])) for p in range(ref.shape[0])):.3g}")
+
+
+@pytest.fixture(scope="module")
+def qwen3_file(tmp_path_factory):
+    path = tmp_path_factory.mktemp("model") / "tiny-qwen3.gguf"
+    W, cfg = write_tiny_qwen3(path, seed=1)
+    return path, W, cfg
+
+
+def test_load_config_and_exact_upload(qwen3_file):
+    path, W, cfg = qwen3_file
+    with M.Model(path, max_ctx=CTX) as m:
+        c = m.config
+        assert (c["n_layers"], c["embed_dim"], c["ff_dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"],
+                c["vocab_size"], c["max_ctx"]) == (2, 512, 768, 4, 2, 128, 1024, CTX)
+        assert c["rope_freq_base"] == np.float32(1e6) and c["rms_eps"] == np.float32(1e-6)
+        assert c["has_qk_norm"] == 1 and c["has_qkv_bias"] == 0
+        for name, a in W.items():
+            assert m.read_tensor(name) == np.ascontiguousarray(a).tobytes(), name
+
+
+def test_forward_matches_oracle(oracle, qwen3_file):
+    path, W, cfg = qwen3_file
+    ref, kc, vc = oracle_forward(oracle, W, cfg, TOKENS, CTX)
+    with M.Model(path, max_ctx=CTX) as m:
+        got, greedy = decode(m, TOKENS)
+        check_against_oracle(got, greedy, ref)
+        # the caches hold one binary16 row per position, as the oracle's
+        for layer in range(cfg["n_layers"]):
+            kd, vd = m.kv_cache(layer)
+            n = CTX * cfg["n_kv"] * cfg["head_dim"] * 2
+            k = np.frombuffer(M.device_to_host(kd, n, m.stream), np.float16).reshape(CTX, -1)
+            v = np.frombuffer(M.device_to_host(vd, n, m.stream), np.float16).reshape(CTX, -1)
+            T = len(TOKENS)
+            assert not k[T:].any() and not v[T:].any(), "positions past the last token stay zero"
+            for got_c, ref_c in ((k, kc[layer]), (v, vc[layer])):
+                ref16 = ref_c.view(np.float16)[:T].astype(np.float64)
+                assert np.max(np.abs(got_c[:T] - ref16)) <= E2E_TOL * np.max(np.abs(ref16))
+
+
+def test_reference_sequence_is_bit_identical(qwen3_file):
+    path, _, _ = qwen3_file
+    with M.Model(path, max_ctx=CTX) as m:
+        fused, g1 = decode(m, TOKENS, M.SEQUENCE_FUSED)
+        refseq, g2 = decode(m, TOKENS, M.SEQUENCE_REFERENCE)
+        assert np.array_equal(fused.view(np.uint32), refseq.view(np.uint32)) and g1 == g2
+
+
+def test_qwen2_style_file(oracle, tmp_path):
+    """No QK-norm, q/k/v biases, and no key_length / rope / epsilon keys:
+    the reference's fallbacks (src/model/qwen3.cu:141-176) apply."""
+    path = tmp_path / "qwen2-style.gguf"
+    W, cfg = write_tiny_qwen3(path, seed=2, arch="qwen2", qk_norm=False, bias=True, keys=False)
+    ref, _, _ = oracle_forward(oracle, W, cfg, TOKENS[:5], CTX)
+    with M.Model(path, max_ctx=CTX) as m:
+        c = m.config
+        assert c["head_dim"] == 128 and c["rope_freq_base"] == 10000.0 and c["rms_eps"] == np.float32(1e-5)
+        assert c["has_qk_norm"] == 0 and c["has_qkv_bias"] == cfg["n_layers"]
+        got, greedy = decode(m, TOKENS[:5])
+        check_against_oracle(got, greedy, ref)
+        refseq, _ = decode(m, TOKENS[:5], M.SEQUENCE_REFERENCE)
+        assert np.array_equal(got.view(np.uint32), refseq.view(np.uint32))
+
+
+def test_unaligned_file_gives_the_same_logits(tmp_path):
+    """general.alignment = 2: tensors sit at 2-byte offsets, so the loader
+    places each one in its own aligned slot instead of copying the region."""
+    a, b = tmp_path / "a32.gguf", tmp_path / "a2.gguf"
+    W, _ = write_tiny_qwen3(a, seed=3)
+    write_tiny_qwen3(b, seed=3, alignment=2)
+    with M.Model(a, max_ctx=CTX) as ma, M.Model(b, max_ctx=CTX) as mb:
+        la, _ = decode(ma, TOKENS[:4])
+        lb, _ = decode(mb, TOKENS[:4])
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        for name, arr in W.items():
+            assert mb.read_tensor(name) == np.ascontiguousarray(arr).tobytes(), name
+
+
+def test_forward_rejects_out_of_range_token_and_position(qwen3_file):
+    path, _, _ = qwen3_file
+    with M.Model(path, max_ctx=CTX) as m:
+        for tok, pos in ((-1, 0), (1024, 0), (0, -1), (0, CTX)):
+            with pytest.raises(FenceError) as e:
+                m.forward(tok, pos)
+            assert e.value.status == EINVAL
+        m.forward(1023, CTX - 1)  # the last valid token and position
+
+
+def test_two_models_are_independent(qwen3_file, tmp_path):
+    path, _, _ = qwen3_file
+    other = tmp_path / "other.gguf"
+    write_tiny_qwen3(other, seed=4)
+    with M.Model(path, max_ctx=CTX) as m1:
+        l1, _ = decode(m1, TOKENS[:3])
+        with M.Model(other, max_ctx=CTX) as m2:
+            decode(m2, TOKENS[:3])
+            again, _ = decode(m1, TOKENS[:3])
+        assert np.array_equal(l1.view(np.uint32), again.view(np.uint32))
+    assert os.path.exists(path)
