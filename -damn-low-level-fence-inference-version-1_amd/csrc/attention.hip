@@ -54,7 +54,8 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // of a sub-chunk are loaded together with its K rows, before phase A.
 // FINAL: one split, write the output; else write (m, l, o) partials to ws.
 template <int GT, bool FINAL>
-__global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict__ out, float* __restrict__ ws,
+__global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict__ out, uint16_t* __restrict__ out16,
+                                                              float* __restrict__ ws,
                                                               const float* __restrict__ q,
                                                               const uint16_t* __restrict__ kc,
                                                               const uint16_t* __restrict__ vc, int n_q, int n_kv,
@@ -192,7 +193,9 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         const float l = hl[g];
         const int h = h0 + g;
         if constexpr (FINAL) {
-            out[static_cast<int64_t>(h) * HD + d] = l == 0.0f ? 0.0f : acc / l;
+            const float r = l == 0.0f ? 0.0f : acc / l;
+            if (out) out[static_cast<int64_t>(h) * HD + d] = r;
+            if (out16) out16[static_cast<int64_t>(h) * HD + d] = f32_to_f16_bits(r);
         } else {
             // partial of (head h, split): [m, l, o[HD]]
             float* p = ws + (static_cast<int64_t>(h) * gridDim.y + split) * (HD + 2);
@@ -210,8 +213,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
 // thread sums c_s * o_s[d] with its loads issued eight at a time.
 constexpr int kMaxMergeSplits = 1024;
 
-__global__ __launch_bounds__(128) void attn_merge_kernel(float* __restrict__ out, const float* __restrict__ ws,
-                                                         int splits) {
+__global__ __launch_bounds__(128) void attn_merge_kernel(float* __restrict__ out, uint16_t* __restrict__ out16,
+                                                         const float* __restrict__ ws, int splits) {
     constexpr int HD = 128;
     __shared__ float cw[kMaxMergeSplits];
     __shared__ float red[2];
@@ -242,12 +245,15 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(float* __restrict__ out
         for (int b = 0; b < kBatch; ++b)
             if (s0 + b < splits) o = __builtin_fmaf(cw[s0 + b], v[b], o);
     }
-    out[static_cast<int64_t>(h) * HD + d] = l == 0.0f ? 0.0f : o / l;
+    const float r = l == 0.0f ? 0.0f : o / l;
+    if (out) out[static_cast<int64_t>(h) * HD + d] = r;
+    if (out16) out16[static_cast<int64_t>(h) * HD + d] = f32_to_f16_bits(r);
 }
 
 // Any head_dim / alignment: one workgroup per query head, the reference's
 // three passes with the scores kept in ws (n_q x max_ctx, as the reference).
-__global__ __launch_bounds__(256) void attn_generic_kernel(float* __restrict__ out, float* __restrict__ ws,
+__global__ __launch_bounds__(256) void attn_generic_kernel(float* __restrict__ out, uint16_t* __restrict__ out16,
+                                                           float* __restrict__ ws,
                                                            const float* __restrict__ q,
                                                            const uint16_t* __restrict__ kc,
                                                            const uint16_t* __restrict__ vc, int hd, int n_q,
@@ -284,7 +290,9 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(float* __restrict__ o
                                  static_cast<float>(__builtin_bit_cast(
                                      _Float16, vc[t * kv_dim + static_cast<int64_t>(kvh) * hd + d])),
                                  acc);
-        out[static_cast<int64_t>(h) * hd + d] = seq_len > 0 ? acc : 0.0f;
+        const float r = seq_len > 0 ? acc : 0.0f;
+        if (out) out[static_cast<int64_t>(h) * hd + d] = r;
+        if (out16) out16[static_cast<int64_t>(h) * hd + d] = f32_to_f16_bits(r);
     }
 }
 
@@ -356,7 +364,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int* __restrict__ result, 
 }
 
 template <int GT>
-int launch_split(float* out, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc, int n_q, int n_kv,
+int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc, int n_q, int n_kv,
                  int seq_len, int64_t ws_floats, float scale, hipStream_t s) {
     constexpr int HD = 128;
     const int group = n_q / n_kv;
@@ -374,25 +382,28 @@ int launch_split(float* out, float* ws, const float* q, const uint16_t* kc, cons
     const int chunk = static_cast<int>((seq_len + splits - 1) / splits);
     const dim3 grid(static_cast<unsigned>(base_wg), static_cast<unsigned>(splits));
     if (splits == 1)
-        return launch(attn_split_kernel<GT, true>, grid, dim3(kThreads), 0, s, out, ws, q, kc, vc, n_q, n_kv, seq_len,
-                      chunk, scale);
-    if (int st = launch(attn_split_kernel<GT, false>, grid, dim3(kThreads), 0, s, out, ws, q, kc, vc, n_q, n_kv,
-                        seq_len, chunk, scale))
+        return launch(attn_split_kernel<GT, true>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc, n_q, n_kv,
+                      seq_len, chunk, scale);
+    if (int st = launch(attn_split_kernel<GT, false>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc, n_q,
+                        n_kv, seq_len, chunk, scale))
         return st;
-    return launch(attn_merge_kernel, dim3(static_cast<unsigned>(n_q)), dim3(HD), 0, s, out, ws,
+    return launch(attn_merge_kernel, dim3(static_cast<unsigned>(n_q)), dim3(HD), 0, s, out, out16, ws,
                   static_cast<int>(splits));
 }
 
 }  // namespace
 
-int gqa_attention_launch(float* out, const float* q, const void* kcv, const void* vcv, int hd, int n_q, int n_kv,
-                         int seq_len, int max_ctx, float* ws, hipStream_t s) {
-    if (!out || !q || !kcv || !vcv || hd <= 0 || n_q <= 0 || n_kv <= 0 || (n_q % n_kv) != 0)
+// out (fp32) and/or out16 (its binary16 rounding, the f32_to_f16 of
+// src/model/qwen3.cu:308 fused) receive the result.
+int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void* kcv, const void* vcv, int hd,
+                         int n_q, int n_kv, int seq_len, int max_ctx, float* ws, hipStream_t s) {
+    if ((!out && !out16) || !q || !kcv || !vcv || hd <= 0 || n_q <= 0 || n_kv <= 0 || (n_q % n_kv) != 0)
         return FENCE_ERROR_INVALID_VALUE;
+    if (out16 && !aligned(out16, 2)) return FENCE_ERROR_INVALID_VALUE;
     if (seq_len < 0 || max_ctx < 1 || seq_len > max_ctx) return FENCE_ERROR_INVALID_VALUE;
     const uint16_t* kc = static_cast<const uint16_t*>(kcv);
     const uint16_t* vc = static_cast<const uint16_t*>(vcv);
-    if (!aligned(out, 4) || !aligned(q, 4) || !aligned(kc, 2) || !aligned(vc, 2) || (ws && !aligned(ws, 4)))
+    if ((out && !aligned(out, 4)) || !aligned(q, 4) || !aligned(kc, 2) || !aligned(vc, 2) || (ws && !aligned(ws, 4)))
         return FENCE_ERROR_INVALID_VALUE;
     const float scale = 1.0f / sqrtf(static_cast<float>(hd));
     const float scale2 = scale * 1.44269504088896340736f;  // scores in log2 units for exp2
@@ -400,17 +411,19 @@ int gqa_attention_launch(float* out, const float* q, const void* kcv, const void
     const int group = n_q / n_kv;
     const bool vec = hd == 128 && aligned(q, 16) && aligned(kc, 16) && aligned(vc, 16);
     if (vec) {
-        if (FENCE_ATTN_GT_MAX == 1) return launch_split<1>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (FENCE_ATTN_GT_MAX == 1)
+            return launch_split<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
         if (FENCE_ATTN_GT_MAX == 2 && group >= 2)
-            return launch_split<2>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
-        if (group >= 4) return launch_split<4>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
-        if (group == 2) return launch_split<2>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
-        if (group == 1) return launch_split<1>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
-        return launch_split<4>(out, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);  // group 3: masked
+            return launch_split<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (group >= 4) return launch_split<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (group == 2) return launch_split<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        if (group == 1) return launch_split<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        // group 3: masked
+        return launch_split<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
     }
     if (!ws) return FENCE_ERROR_INVALID_VALUE;  // the generic path keeps scores in score_buf
-    return launch(attn_generic_kernel, dim3(static_cast<unsigned>(n_q)), dim3(256), 0, s, out, ws, q, kc, vc, hd,
-                  n_q, n_kv, seq_len, max_ctx, scale);
+    return launch(attn_generic_kernel, dim3(static_cast<unsigned>(n_q)), dim3(256), 0, s, out, out16, ws, q, kc, vc,
+                  hd, n_q, n_kv, seq_len, max_ctx, scale);
 }
 
 int store_kv_launch(void* kcv, void* vcv, const float* k, const float* v, int pos, int kv_dim, int max_ctx,
@@ -442,8 +455,17 @@ extern "C" int fence_argmax(const float* x, int* result, int n, hipStream_t stre
 extern "C" int fence_gqa_attention(float* attn_out, const float* q, const void* k_cache, const void* v_cache,
                                    int head_dim, int n_q_heads, int n_kv_heads, int seq_len, int max_ctx,
                                    float* score_buf, hipStream_t stream) {
-    return fence::gqa_attention_launch(attn_out, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, seq_len,
-                                       max_ctx, score_buf, stream);
+    if (!attn_out) return FENCE_ERROR_INVALID_VALUE;
+    return fence::gqa_attention_launch(attn_out, nullptr, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads,
+                                       seq_len, max_ctx, score_buf, stream);
+}
+
+extern "C" int fence_gqa_attention_f16(float* attn_out, void* out_f16, const float* q, const void* k_cache,
+                                       const void* v_cache, int head_dim, int n_q_heads, int n_kv_heads, int seq_len,
+                                       int max_ctx, float* score_buf, hipStream_t stream) {
+    if (!out_f16) return FENCE_ERROR_INVALID_VALUE;
+    return fence::gqa_attention_launch(attn_out, static_cast<uint16_t*>(out_f16), q, k_cache, v_cache, head_dim,
+                                       n_q_heads, n_kv_heads, seq_len, max_ctx, score_buf, stream);
 }
 
 extern "C" int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v, int pos, int kv_dim,

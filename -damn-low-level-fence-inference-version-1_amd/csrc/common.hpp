@@ -41,16 +41,31 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 // binary32 -> binary16 by the hardware conversion (v_cvt_f16_f32): round to
 // nearest even, overflow to inf, binary16 subnormals kept (the default MODE).
+// The empty asm makes v an fp32 value first: otherwise the compiler may fold
+// the multiply that produced it and the conversion into one v_fma_mixlo_f16,
+// which rounds the exact product to binary16 once -- not what the reference's
+// chain does (an fp32 result in memory, then f32_to_f16), and different
+// whenever the fp32 rounding lands on a binary16 tie.
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    asm volatile("" : "+v"(v));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
-// Four binary16 values rounded from a float4, one 64-bit store (p 8-byte aligned).
+// Four binary16 values rounded from a float4, one 64-bit store (p 8-byte
+// aligned); fp32 first, as above.
 template <bool NT>
 __device__ __forceinline__ void st_h4(uint16_t* p, f4 v) {
+    asm volatile("" : "+v"(v));
     const h4 h = __builtin_convertvector(v, h4);
     if constexpr (NT) __builtin_nontemporal_store(h, reinterpret_cast<h4*>(p));
     else *reinterpret_cast<h4*>(p) = h;
+}
+
+// silu(g) * u as silu_elementwise_mul computes it, src/kernels/ops.cuh:183-202.
+// Every kernel that produces SwiGLU activations uses this one expression, so
+// fused and unfused paths round identically.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return (g / (1.0f + expf(-g))) * u;
 }
 
 __device__ __forceinline__ float dot4(f4 a) {

@@ -38,6 +38,16 @@
 #ifndef FENCE_GEMV_Q6K_PREFETCH
 #define FENCE_GEMV_Q6K_PREFETCH 0
 #endif
+// How a row's blocks are split over waves (see q6_plan): 0 up to four passes
+// (16 blocks) per wave, 1 up to two, 2 one pass where the row allows.
+#ifndef FENCE_GEMV_Q6K_SPLIT
+#define FENCE_GEMV_Q6K_SPLIT 0
+#endif
+// 1: an occupancy-sized grid of workgroups looping over row groups;
+// 0: one workgroup per row group.
+#ifndef FENCE_GEMV_Q6K_RESIDENT
+#define FENCE_GEMV_Q6K_RESIDENT 1
+#endif
 
 namespace fence {
 namespace {
@@ -132,21 +142,53 @@ __device__ __forceinline__ void load_x(uint32_t (&xh)[PASSES][8], float (&kb)[PA
     }
 }
 
+// A launch's matrices: up to kMaxMats row blocks that share x and K, their
+// rows numbered one after another (matrix i holds rows [end[i-1], end[i])).
+// PAIR: two matrices of M rows each, gate and up, combined per row into
+// act = silu(gate x) * (up x), written as binary16 (act16) and optionally
+// fp32 (act32) -- src/model/qwen3.cu:328-336 in one pass.
+constexpr int kMaxMats = 4;
+struct Q6Job {
+    const uint8_t* W[kMaxMats];
+    float* y[kMaxMats];
+    const float* bias[kMaxMats];
+    int end[kMaxMats];
+    int n;
+    uint16_t* act16;
+    float* act32;
+};
+
+// Matrix of global row r (wave-uniform), and r's row within it.
+__device__ __forceinline__ int mat_of(const Q6Job& job, int64_t r, int64_t* lr) {
+    int m = 0;
+#pragma unroll
+    for (int k = 0; k < kMaxMats - 1; ++k) m += (k < job.n - 1 && r >= job.end[k]) ? 1 : 0;
+    *lr = r - (m ? job.end[m - 1] : 0);
+    return m;
+}
+
+// Waves of a staged workgroup: 4, or 8 for a gate/up pair whose rows take
+// four waves each.
+template <int WPR, bool PAIR>
+constexpr int staged_waves() { return PAIR && WPR == 4 ? 8 : 4; }
+
 // Staged kernel.  WPR waves per row (1, 2 or 4), each over at most 4 * PASSES
-// <= 16 blocks.  LDS: 4 wave buffers of kSegBytes + red[4].
-template <int PASSES, int WPR, bool PF>
-__global__ __launch_bounds__(kThreads) void gemv_q6k_staged_kernel(float* __restrict__ y,
-                                                                   const uint8_t* __restrict__ W,
-                                                                   const uint16_t* __restrict__ x16,
-                                                                   const float* __restrict__ bias, int M,
-                                                                   int nb) {
+// <= 16 blocks.  LDS: one buffer of kSegBytes per wave + red[].  A workgroup
+// of NW waves takes NW / WPR rows per group; with PAIR the first half of them
+// are gate rows and the second half the same rows of up.
+template <int PASSES, int WPR, bool PF, bool PAIR, bool MULTI>
+__global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_staged_kernel(
+    const Q6Job job, const uint16_t* __restrict__ x16, int nb) {
+    constexpr int NW = staged_waves<WPR, PAIR>();
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
     constexpr int kChunkSlots = (kSegBytes / 16 + kWave - 1) / kWave;
-    constexpr int kRowsPerGroup = 4 / WPR;
+    constexpr int kRowsPerGroup = NW / WPR;
+    constexpr int kOutPerGroup = PAIR ? kRowsPerGroup / 2 : kRowsPerGroup;
+    static_assert(!PAIR || kRowsPerGroup >= 2, "a pair needs two rows per group");
     constexpr uint32_t kPassBytes = 4 * kBlockBytes;  // 840: a multiple of 4
-    __shared__ __align__(16) uint8_t lds[4 * kBufBytes];
-    __shared__ float red[4];
+    __shared__ __align__(16) uint8_t lds[NW * kBufBytes];
+    __shared__ float red[NW];
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));  // wave-uniform
     const int seg = wid % WPR;
@@ -156,6 +198,7 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_staged_kernel(float* __rest
     int b0, b1;
     segment(nb, seg, WPR, &b0, &b1);
     const int64_t row_bytes = static_cast<int64_t>(nb) * kBlockBytes;
+    const int64_t n_out = PAIR ? job.end[0] : job.end[job.n - 1];  // rows (PAIR: output rows)
 
     uint32_t xh[PASSES][8];
     float kb[PASSES][4];
@@ -168,20 +211,34 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_staged_kernel(float* __rest
     const uint32_t lane_sc = 192 + 8 * h + (j >> 2);  // column 0's scale byte
     const uint32_t blk_off = static_cast<uint32_t>(bslot) * kBlockBytes;
 
-    // The 16-byte chunks covering group g's segment: [a0, a0 + 16 * nch).
-    auto seg_of = [&](int64_t g, int64_t* a0, int* nch, uint32_t* delta) {
-        const int64_t r = g * kRowsPerGroup + rslot;
-        const int64_t rr = r < M ? r : M - 1;  // clamped: a prefetch past the last row stays inside W
-        const int64_t start = rr * row_bytes + static_cast<int64_t>(b0) * kBlockBytes;
-        const int64_t end = rr * row_bytes + static_cast<int64_t>(b1) * kBlockBytes;
+    // The row this wave computes in group g: its output index o (a global row
+    // without PAIR), matrix m and row lr within the matrix; o >= n_out past the end.
+    auto row_of = [&](int64_t g, int64_t* o, int* m, int64_t* lr) {
+        if constexpr (PAIR) {
+            *o = g * kOutPerGroup + rslot % kOutPerGroup;
+            *m = rslot / kOutPerGroup;
+            *lr = *o < n_out ? *o : n_out - 1;  // clamped: loads past the end stay inside W
+        } else if constexpr (MULTI) {
+            *o = g * kRowsPerGroup + rslot;
+            *m = mat_of(job, *o < n_out ? *o : n_out - 1, lr);
+        } else {
+            *o = g * kRowsPerGroup + rslot;
+            *m = 0;
+            *lr = *o < n_out ? *o : n_out - 1;
+        }
+    };
+    // The 16-byte chunks covering the segment: [a0, a0 + 16 * nch) of job.W[m].
+    auto seg_of = [&](int64_t lr, int64_t* a0, int* nch, uint32_t* delta) {
+        const int64_t start = lr * row_bytes + static_cast<int64_t>(b0) * kBlockBytes;
+        const int64_t end = lr * row_bytes + static_cast<int64_t>(b1) * kBlockBytes;
         *a0 = start & ~int64_t(15);
         *nch = static_cast<int>((end - *a0 + 15) >> 4);
         *delta = static_cast<uint32_t>(start - *a0);
     };
     // Loads of one segment's chunks: clamped and opaque offsets, so every
     // load is issued unconditionally in scalar-base + VGPR-offset form.
-    auto load_seg = [&](int64_t a0, int nch, u4* ch) {
-        const uint8_t* src = W + a0;
+    auto load_seg = [&](const uint8_t* Wm, int64_t a0, int nch, u4* ch) {
+        const uint8_t* src = Wm + a0;
 #pragma unroll
         for (int k = 0; k < kChunkSlots; ++k) {
             const int cc = lane + kWave * k;
@@ -195,11 +252,17 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_staged_kernel(float* __rest
     int nchn;
     uint32_t deltan;
     if constexpr (PF) {
-        seg_of(blockIdx.x, &a0n, &nchn, &deltan);
-        load_seg(a0n, nchn, ch);
+        int64_t o, lr;
+        int m;
+        row_of(blockIdx.x, &o, &m, &lr);
+        seg_of(lr, &a0n, &nchn, &deltan);
+        load_seg(job.W[m], a0n, nchn, ch);
     }
-    for (int64_t g = blockIdx.x; g * kRowsPerGroup < M; g += gridDim.x) {
-        const int64_t r = g * kRowsPerGroup + rslot;  // wave-uniform
+    for (int64_t g = blockIdx.x; g * kOutPerGroup < n_out; g += gridDim.x) {
+        int64_t o, lr;
+        int m;
+        row_of(g, &o, &m, &lr);
+        const bool valid = o < n_out;  // wave-uniform
         float part = 0.0f;
         int64_t a0;
         int nch;
@@ -207,10 +270,10 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_staged_kernel(float* __rest
         if constexpr (PF) {
             a0 = a0n, nch = nchn, delta = deltan;
         } else {
-            seg_of(g, &a0, &nch, &delta);
-            load_seg(a0, nch, ch);
+            seg_of(lr, &a0, &nch, &delta);
+            load_seg(job.W[m], a0, nch, ch);
         }
-        if (r < M) {
+        if (valid) {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int k = 0; k < kChunkSlots; ++k) {
@@ -223,11 +286,14 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_staged_kernel(float* __rest
         }
         if constexpr (PF) {
             // the next group's loads fly while this one is computed from LDS
-            seg_of(g + gridDim.x, &a0n, &nchn, &deltan);
-            load_seg(a0n, nchn, ch);
+            int64_t on_, lrn;
+            int mn;
+            row_of(g + gridDim.x, &on_, &mn, &lrn);
+            seg_of(lrn, &a0n, &nchn, &deltan);
+            load_seg(job.W[mn], a0n, nchn, ch);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (r < M) {
+        if (valid) {
             // The lane's block starts at `base` in the buffer for pass 0 and
             // 840 bytes later per pass; every dword it reads has the same
             // offset mod 4, so one aligned base and one shift serve them all.
@@ -255,75 +321,112 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_staged_kernel(float* __rest
             }
             part = wave_sum(part);
         }
-        if constexpr (WPR == 1) {
-            if (r < M && lane == 0) y[r] = bias ? part + bias[r] : part;
+        if constexpr (!PAIR && WPR == 1) {
+            if (valid && lane == 0) {
+                const float* bm = job.bias[m];
+                job.y[m][lr] = bm ? part + bm[lr] : part;
+            }
         } else {
             if (lane == 0) red[wid] = part;
             __syncthreads();
-            if (seg == 0 && lane == 0 && r < M) {
-                float t = red[wid];
+            if constexpr (PAIR) {
+                if (seg == 0 && rslot < kOutPerGroup && lane == 0 && valid) {
+                    float gs = red[wid], us = red[wid + kOutPerGroup * WPR];
 #pragma unroll
-                for (int s = 1; s < WPR; ++s) t += red[wid + s];
-                y[r] = bias ? t + bias[r] : t;
+                    for (int s = 1; s < WPR; ++s) gs += red[wid + s], us += red[wid + kOutPerGroup * WPR + s];
+                    const float act = silu_mul(gs, us);
+                    job.act16[o] = f32_to_f16_bits(act);
+                    if (job.act32) job.act32[o] = act;
+                }
+            } else {
+                if (seg == 0 && lane == 0 && valid) {
+                    float t = red[wid];
+#pragma unroll
+                    for (int s = 1; s < WPR; ++s) t += red[wid + s];
+                    const float* bm = job.bias[m];
+                    job.y[m][lr] = bm ? t + bm[lr] : t;
+                }
             }
             __syncthreads();  // red[] is rewritten by the next group
         }
     }
 }
 
-// Direct kernel for any alignment and any K: the same lanes, the dwords read
-// straight from global memory (two aligned dwords each, realigned).
-__global__ __launch_bounds__(kThreads) void gemv_q6k_direct_kernel(float* __restrict__ y,
-                                                                   const uint8_t* __restrict__ W,
-                                                                   const uint16_t* __restrict__ x16,
-                                                                   const float* __restrict__ bias, int M,
-                                                                   int nb) {
-    const int lane = threadIdx.x & (kWave - 1);
+// y . row lr of Wm, summed over the wave (lane 0 holds it): the direct
+// kernel's dwords come straight from global memory, two aligned dwords each,
+// realigned.
+__device__ __forceinline__ float direct_row(const uint8_t* Wm, const uint16_t* x16, int64_t lr, int nb, int lane) {
     const int bslot = lane >> 4, h = (lane >> 3) & 1, j = lane & 7;
     const int64_t row_bytes = static_cast<int64_t>(nb) * kBlockBytes;
+    float part = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 4) {
+        const int b = b0 + bslot;
+        if (b < nb) {
+            const uint8_t* blk = Wm + lr * row_bytes + static_cast<int64_t>(b) * kBlockBytes;
+            auto rd = [&](int off) {
+                const uint8_t* p = blk + off;
+                const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+                const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3);
+                // both dwords lie inside the 210-byte block for every offset used
+                return sh ? __builtin_amdgcn_alignbyte(w[1], w[0], sh) : w[0];
+            };
+            const uint32_t a = rd(64 * h + 4 * j), bq = rd(64 * h + 32 + 4 * j), c = rd(128 + 32 * h + 4 * j);
+            int sc[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sc[q] = static_cast<int8_t>(blk[192 + 8 * h + (j >> 2) + 2 * q]);
+            const uint16_t dbits = static_cast<uint16_t>(blk[208] | (blk[209] << 8));
+            uint32_t xh[8];
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const int e = 256 * b + 128 * h + 32 * cc + 4 * j;
+                xh[2 * cc] = x16[e] | (static_cast<uint32_t>(x16[e + 1]) << 16);
+                xh[2 * cc + 1] = x16[e + 2] | (static_cast<uint32_t>(x16[e + 3]) << 16);
+            }
+            float kbc[4];
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) kbc[cc] = q6_col_bias(xh[2 * cc], xh[2 * cc + 1]);
+            const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+            part += q6_lane_dot(q6_unpack(a, bq, c), xh, kbc, sc, d);
+        }
+    }
+    return wave_sum(part);
+}
+
+// Direct kernel for any alignment and any K: one wave per row (PAIR: per
+// output row, its gate row then its up row).
+template <bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemv_q6k_direct_kernel(const Q6Job job,
+                                                                   const uint16_t* __restrict__ x16, int nb) {
+    const int lane = threadIdx.x & (kWave - 1);
     const int64_t wave = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) / kWave;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
-    for (int64_t r = wave; r < M; r += nwaves) {
-        float part = 0.0f;
-        for (int b0 = 0; b0 < nb; b0 += 4) {
-            const int b = b0 + bslot;
-            if (b < nb) {
-                const uint8_t* blk = W + r * row_bytes + static_cast<int64_t>(b) * kBlockBytes;
-                auto rd = [&](int off) {
-                    const uint8_t* p = blk + off;
-                    const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
-                    const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3);
-                    // both dwords lie inside the 210-byte block for every offset used
-                    return sh ? __builtin_amdgcn_alignbyte(w[1], w[0], sh) : w[0];
-                };
-                const uint32_t a = rd(64 * h + 4 * j), bq = rd(64 * h + 32 + 4 * j), c = rd(128 + 32 * h + 4 * j);
-                int sc[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) sc[q] = static_cast<int8_t>(blk[192 + 8 * h + (j >> 2) + 2 * q]);
-                const uint16_t dbits = static_cast<uint16_t>(blk[208] | (blk[209] << 8));
-                uint32_t xh[8];
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc) {
-                    const int e = 256 * b + 128 * h + 32 * cc + 4 * j;
-                    xh[2 * cc] = x16[e] | (static_cast<uint32_t>(x16[e + 1]) << 16);
-                    xh[2 * cc + 1] = x16[e + 2] | (static_cast<uint32_t>(x16[e + 3]) << 16);
-                }
-                float kbc[4];
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc) kbc[cc] = q6_col_bias(xh[2 * cc], xh[2 * cc + 1]);
-                const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
-                part += q6_lane_dot(q6_unpack(a, bq, c), xh, kbc, sc, d);
+    const int64_t n_out = PAIR ? job.end[0] : job.end[job.n - 1];
+    for (int64_t r = wave; r < n_out; r += nwaves) {
+        if constexpr (PAIR) {
+            const float gs = direct_row(job.W[0], x16, r, nb, lane);
+            const float us = direct_row(job.W[1], x16, r, nb, lane);
+            if (lane == 0) {
+                const float act = silu_mul(gs, us);
+                job.act16[r] = f32_to_f16_bits(act);
+                if (job.act32) job.act32[r] = act;
+            }
+        } else {
+            int64_t lr;
+            const int m = mat_of(job, r, &lr);
+            const float part = direct_row(job.W[m], x16, lr, nb, lane);
+            if (lane == 0) {
+                const float* bm = job.bias[m];
+                job.y[m][lr] = bm ? part + bm[lr] : part;
             }
         }
-        part = wave_sum(part);
-        if (lane == 0) y[r] = bias ? part + bias[r] : part;
     }
 }
 
+// A resident grid for `kernel` of `threads` per workgroup: CUs x the
+// occupancy per CU (cached per device in `cache`), at most `groups`.
 template <class Kernel>
-int launch_grid(Kernel kernel, int64_t groups, float* y, const uint8_t* W, const uint16_t* x, const float* bias,
-                int M, int nb, hipStream_t s) {
-    static std::atomic<int> cache[64];
+int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t groups, const Q6Job& job,
+                const uint16_t* x, int nb, hipStream_t s) {
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e);
     if (dev < 0 || dev >= 64) return FENCE_ERROR_INVALID_VALUE;
@@ -332,44 +435,90 @@ int launch_grid(Kernel kernel, int64_t groups, float* y, const uint8_t* W, const
         int cus = 0, per_cu = 0;
         if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev); e != hipSuccess)
             return hip_status(e);
-        if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0);
+        if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0);
             e != hipSuccess)
             return hip_status(e);
         g = cus * (per_cu > 0 ? per_cu : 1);
         cache[dev].store(g, std::memory_order_relaxed);
     }
+    if (!FENCE_GEMV_Q6K_RESIDENT) g = 0x7fffffff;
     const unsigned grid = static_cast<unsigned>(groups < g ? groups : g);
-    return launch(kernel, dim3(grid), dim3(kThreads), 0, s, y, W, x, bias, M, nb);
+    return launch(kernel, dim3(grid), dim3(threads), 0, s, job, x, nb);
 }
 
-template <int PASSES, int WPR>
-int launch_staged(float* y, const uint8_t* W, const uint16_t* x, const float* bias, int M, int nb, hipStream_t s) {
-    constexpr int rows_per_group = 4 / WPR;
-    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, FENCE_GEMV_Q6K_PREFETCH != 0>,
-                       (M + rows_per_group - 1) / rows_per_group, y, W, x, bias, M, nb, s);
+template <int PASSES, int WPR, bool PAIR, bool MULTI>
+int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, hipStream_t s) {
+    static std::atomic<int> cache[64];
+    constexpr int nw = staged_waves<WPR, PAIR>();
+    constexpr int out_per_group = PAIR ? nw / WPR / 2 : nw / WPR;
+    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, FENCE_GEMV_Q6K_PREFETCH != 0, PAIR, MULTI>, kWave * nw,
+                       cache, (n_out + out_per_group - 1) / out_per_group, job, x, nb, s);
+}
+
+// (PASSES, WPR) of a row of nb blocks: WPR waves per row, each over at most
+// 4 * PASSES blocks.  It depends on nb alone, so every matrix of a multi or
+// pair launch sums its rows in the same order as its own launch would.
+template <bool PAIR, bool MULTI>
+int launch_nb(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, hipStream_t s) {
+    if (FENCE_GEMV_Q6K_SPLIT == 2) {
+        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 8) return launch_staged<1, 2, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 16) return launch_staged<1, 4, PAIR, MULTI>(job, n_out, x, nb, s);
+    } else if (FENCE_GEMV_Q6K_SPLIT == 1) {
+        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 16) return launch_staged<2, 2, PAIR, MULTI>(job, n_out, x, nb, s);
+    } else {
+        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 12) return launch_staged<3, 1, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 16) return launch_staged<4, 1, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 24) return launch_staged<3, 2, PAIR, MULTI>(job, n_out, x, nb, s);
+    }
+    if (FENCE_GEMV_Q6K_SPLIT == 0 && nb <= 32) return launch_staged<4, 2, PAIR, MULTI>(job, n_out, x, nb, s);
+    if (nb <= 32) return launch_staged<2, 4, PAIR, MULTI>(job, n_out, x, nb, s);
+    if (nb <= 48) return launch_staged<3, 4, PAIR, MULTI>(job, n_out, x, nb, s);
+    return launch_staged<4, 4, PAIR, MULTI>(job, n_out, x, nb, s);
+}
+
+template <bool PAIR>
+int launch_direct(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, hipStream_t s) {
+    static std::atomic<int> cache[64];
+    return launch_grid(gemv_q6k_direct_kernel<PAIR>, kThreads, cache, (n_out + 3) / 4, job, x, nb, s);
+}
+
+// Checks and dispatch of a job whose matrices, rows and outputs are filled in.
+int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s) {
+    if (K <= 0 || (K % 256) != 0 || !xv || !aligned(xv, 2)) return FENCE_ERROR_INVALID_VALUE;
+    const uint16_t* x = static_cast<const uint16_t*>(xv);
+    const int nb = K / 256;
+    const int64_t n_out = pair ? job.end[0] : job.end[job.n - 1];
+    if (n_out == 0) return FENCE_SUCCESS;
+    bool staged = nb <= 4 * kMaxSegBlocks;
+    int prev = 0;
+    for (int i = 0; i < job.n; ++i) {
+        const int rows = job.end[i] - prev;
+        prev = job.end[i];
+        if (rows == 0) continue;
+        staged = staged && aligned(job.W[i], 16) && (static_cast<int64_t>(rows) * nb) % 8 == 0;
+    }
+    if (pair) return staged ? launch_nb<true, false>(job, n_out, x, nb, s) : launch_direct<true>(job, n_out, x, nb, s);
+    if (!staged) return launch_direct<false>(job, n_out, x, nb, s);
+    return job.n > 1 ? launch_nb<false, true>(job, n_out, x, nb, s) : launch_nb<false, false>(job, n_out, x, nb, s);
 }
 
 int gemv_q6k_launch(float* y, const void* Wv, const void* xv, const float* bias, int M, int K, hipStream_t s) {
     if (M < 0 || K < 0 || (K % 256) != 0) return FENCE_ERROR_INVALID_VALUE;
     if (M == 0) return FENCE_SUCCESS;
     if (K == 0 || !y || !Wv || !xv) return FENCE_ERROR_INVALID_VALUE;
-    const uint8_t* W = static_cast<const uint8_t*>(Wv);
-    const uint16_t* x = static_cast<const uint16_t*>(xv);
-    if (!aligned(W, 2) || !aligned(x, 2) || !aligned(y, 4) || (bias && !aligned(bias, 4)))
-        return FENCE_ERROR_INVALID_VALUE;
-    const int nb = K / 256;
-    const bool staged = aligned(W, 16) && (static_cast<int64_t>(M) * nb) % 8 == 0 && nb <= 4 * kMaxSegBlocks;
-    if (staged) {
-        if (nb <= 4) return launch_staged<1, 1>(y, W, x, bias, M, nb, s);
-        if (nb <= 8) return launch_staged<2, 1>(y, W, x, bias, M, nb, s);
-        if (nb <= 12) return launch_staged<3, 1>(y, W, x, bias, M, nb, s);
-        if (nb <= 16) return launch_staged<4, 1>(y, W, x, bias, M, nb, s);
-        if (nb <= 24) return launch_staged<3, 2>(y, W, x, bias, M, nb, s);
-        if (nb <= 32) return launch_staged<4, 2>(y, W, x, bias, M, nb, s);
-        if (nb <= 48) return launch_staged<3, 4>(y, W, x, bias, M, nb, s);
-        return launch_staged<4, 4>(y, W, x, bias, M, nb, s);
-    }
-    return launch_grid(gemv_q6k_direct_kernel, (static_cast<int64_t>(M) + 3) / 4, y, W, x, bias, M, nb, s);
+    if (!aligned(Wv, 2) || !aligned(y, 4) || (bias && !aligned(bias, 4))) return FENCE_ERROR_INVALID_VALUE;
+    Q6Job job{};
+    job.W[0] = static_cast<const uint8_t*>(Wv);
+    job.y[0] = y;
+    job.bias[0] = bias;
+    job.end[0] = M;
+    job.n = 1;
+    return gemv_q6k_run(job, xv, K, false, s);
 }
 
 }  // namespace
@@ -383,4 +532,47 @@ extern "C" int fence_gemv_q6k_bias(const void* W, const void* x, const float* bi
                                    hipStream_t stream) {
     if (!bias) return FENCE_ERROR_INVALID_VALUE;
     return fence::gemv_q6k_launch(y, W, x, bias, M, K, stream);
+}
+
+extern "C" int fence_gemv_q6k_multi(int n, const void* const* W, float* const* y, const float* const* bias,
+                                    const int* M, const void* x, int K, hipStream_t stream) {
+    using namespace fence;
+    if (n < 1 || n > kMaxMats || !W || !y || !M) return FENCE_ERROR_INVALID_VALUE;
+    Q6Job job{};
+    int64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+        if (M[i] < 0) return FENCE_ERROR_INVALID_VALUE;
+        if (M[i] > 0 && (!W[i] || !y[i] || !aligned(W[i], 2) || !aligned(y[i], 4) ||
+                         (bias && bias[i] && !aligned(bias[i], 4))))
+            return FENCE_ERROR_INVALID_VALUE;
+        total += M[i];
+        if (total > 0x7fffffff) return FENCE_ERROR_INVALID_VALUE;
+        job.W[i] = static_cast<const uint8_t*>(W[i]);
+        job.y[i] = y[i];
+        job.bias[i] = bias ? bias[i] : nullptr;
+        job.end[i] = static_cast<int>(total);
+    }
+    job.n = n;
+    if (K < 0 || K % 256 != 0) return FENCE_ERROR_INVALID_VALUE;
+    if (total == 0) return FENCE_SUCCESS;
+    return gemv_q6k_run(job, x, K, false, stream);
+}
+
+extern "C" int fence_gemv_q6k_swiglu_f16(const void* W_gate, const void* W_up, const void* x, void* out_f16,
+                                         float* out, int M, int K, hipStream_t stream) {
+    using namespace fence;
+    if (M < 0 || M > 0x3fffffff || K < 0 || K % 256 != 0) return FENCE_ERROR_INVALID_VALUE;
+    if (M == 0) return FENCE_SUCCESS;
+    if (!W_gate || !W_up || !out_f16 || !aligned(W_gate, 2) || !aligned(W_up, 2) || !aligned(out_f16, 2) ||
+        (out && !aligned(out, 4)))
+        return FENCE_ERROR_INVALID_VALUE;
+    Q6Job job{};
+    job.W[0] = static_cast<const uint8_t*>(W_gate);
+    job.W[1] = static_cast<const uint8_t*>(W_up);
+    job.end[0] = M;
+    job.end[1] = 2 * M;  // rows of up follow gate's (row counts for the staging checks)
+    job.n = 2;
+    job.act16 = static_cast<uint16_t*>(out_f16);
+    job.act32 = out;
+    return gemv_q6k_run(job, x, K, true, stream);
 }

@@ -37,6 +37,29 @@ struct InvFreq {
     float v[kMaxHalf];
 };
 
+// Operands of a head-structured op.  qo/qi: q output/input
+// [tokens][nq][hd]; k: [tokens][nkv][hd], in place; wq/wk: norm weights.
+// With kc set (KV store): the rotated k and the matching v [tokens][nkv][hd]
+// are also written as binary16 rows of the caches kc/vc [max_ctx][nkv*hd],
+// at the token's position (store_kv, src/kernels/ops.cuh:419-443); a
+// position outside [0, max_ctx) stores nothing.
+struct HeadArgs {
+    float* qo;
+    const float* qi;
+    float* k;
+    const float* wq;
+    const float* wk;
+    int64_t tokens;
+    int nq, nkv;
+    float eps;
+    const int32_t* positions;
+    int pos0;
+    uint16_t* kc;
+    uint16_t* vc;
+    const float* v;
+    int max_ctx;
+};
+
 namespace {
 
 // sin and cos of an angle given in radians as an exact float (the angle
@@ -51,10 +74,18 @@ __device__ __forceinline__ void sincos_angle(float a, float* s, float* c) {
 }
 
 // MAXS units per lane (exactly: the dispatcher launches MAXS == slots).
-template <int ROPE, int NORM, int G, int MAXS>
-__global__ __launch_bounds__(1024) void head_ops_vec_kernel(
-    float* qo, const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
-    int nkv, float eps, const int32_t* __restrict__ positions, int pos0, InvFreq tab) {
+template <int ROPE, int NORM, int G, int MAXS, bool KV>
+__global__ __launch_bounds__(1024) void head_ops_vec_kernel(const HeadArgs args, InvFreq tab) {
+    float* qo = args.qo;
+    const float* qi = args.qi;
+    float* k = args.k;
+    const float* wq = args.wq;
+    const float* wk = args.wk;
+    const int64_t tokens = args.tokens;
+    const int nq = args.nq, nkv = args.nkv;
+    const float eps = args.eps;
+    const int32_t* __restrict__ positions = args.positions;
+    const int pos0 = args.pos0;
     constexpr int HD = 8 * G;
     constexpr int HALF = 4 * G;
     __shared__ __align__(16) float cs[2 * HALF];  // cos[HALF] then sin[HALF]
@@ -107,6 +138,7 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
         // the values), so the compiler can count them and start the angles
         // while they are in flight.
         f4 a[MAXS], b[MAXS];
+        f4 va_v[KV ? MAXS : 1], vb_v[KV ? MAXS : 1];  // v of the lane's k units (KV store)
 #pragma unroll
         for (int s = 0; s < MAXS; ++s) {
             int u = threadIdx.x + s * T;
@@ -116,6 +148,11 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
             const float* src = (h < nq) ? qrow_in + h * HD : krow + (h - nq) * HD;
             a[s] = ld4<true>(src + 4 * i);
             b[s] = ld4<true>(src + HALF + 4 * i);
+            if constexpr (KV) {  // a q unit reads head 0's v and drops it
+                const float* vsrc = args.v + t * nkv * HD + (h < nq ? 0 : (h - nq) * HD);
+                va_v[s] = ld4<true>(vsrc + 4 * i);
+                vb_v[s] = ld4<true>(vsrc + HALF + 4 * i);
+            }
         }
 
         if constexpr (ROPE != kRopeNone) {
@@ -196,6 +233,15 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
             float* dst = isq ? qrow_out + h * HD : krow + (h - nq) * HD;
             st4<true>(dst + 4 * i, va);
             st4<true>(dst + HALF + 4 * i, vb);
+            if constexpr (KV) {
+                if (!isq && pos >= 0 && pos < args.max_ctx) {
+                    const int64_t at = static_cast<int64_t>(pos) * nkv * HD + (h - nq) * HD;
+                    st_h4<false>(args.kc + at + 4 * i, va);
+                    st_h4<false>(args.kc + at + HALF + 4 * i, vb);
+                    st_h4<false>(args.vc + at + 4 * i, va_v[s]);
+                    st_h4<false>(args.vc + at + HALF + 4 * i, vb_v[s]);
+                }
+            }
         }
         __syncthreads();  // cs[] and red[] are rewritten for the next token
     }
@@ -203,9 +249,17 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(
 
 // Any head_dim and alignment.  One workgroup per token, one wave per head.
 template <int ROPE, int NORM>
-__global__ __launch_bounds__(256) void head_ops_scalar_kernel(
-    float* qo, const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
-    int nkv, int hd, float eps, const int32_t* positions, int pos0, InvFreq tab) {
+__global__ __launch_bounds__(256) void head_ops_scalar_kernel(const HeadArgs args, int hd, InvFreq tab) {
+    float* qo = args.qo;
+    const float* qi = args.qi;
+    float* k = args.k;
+    const float* wq = args.wq;
+    const float* wk = args.wk;
+    const int64_t tokens = args.tokens;
+    const int nq = args.nq, nkv = args.nkv;
+    const float eps = args.eps;
+    const int32_t* positions = args.positions;
+    const int pos0 = args.pos0;
     __shared__ float red[4];
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
@@ -241,8 +295,19 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(
                 for (int e = lane; e < hd; e += kWave) ss += src[e] * src[e];
                 r = rsqrtf(wave_reduce(ss, OpAdd()) / static_cast<float>(hd) + eps);
             }
+            // KV store of this k head: the row of the token's position
+            const bool kv = args.kc && !isq && pos >= 0 && pos < args.max_ctx;
+            const int64_t at = static_cast<int64_t>(pos) * nkv * hd + (h - nq) * hd;
+            if (kv) {
+                const float* vsrc = args.v + t * nkv * hd + (h - nq) * hd;
+                for (int e = lane; e < hd; e += kWave) args.vc[at + e] = f32_to_f16_bits(vsrc[e]);
+            }
             if constexpr (ROPE == kRopeNone) {
-                for (int e = lane; e < hd; e += kWave) dst[e] = wr ? (wr[e] * src[e]) * r : src[e];
+                for (int e = lane; e < hd; e += kWave) {
+                    const float val = wr ? (wr[e] * src[e]) * r : src[e];
+                    dst[e] = val;
+                    if (kv) args.kc[at + e] = f32_to_f16_bits(val);
+                }
             } else {
                 for (int p = lane; p < half; p += kWave) {
                     const int i0 = (ROPE == kRopeNeox) ? p : 2 * p;
@@ -255,8 +320,13 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(
                     }
                     float sn, cn;
                     sincos_angle(static_cast<float>(pos) * tab.v[p], &sn, &cn);
-                    dst[i0] = x0 * cn - x1 * sn;
-                    dst[i1] = x0 * sn + x1 * cn;
+                    const float y0 = x0 * cn - x1 * sn, y1 = x0 * sn + x1 * cn;
+                    dst[i0] = y0;
+                    dst[i1] = y1;
+                    if (kv) {
+                        args.kc[at + i0] = f32_to_f16_bits(y0);
+                        args.kc[at + i1] = f32_to_f16_bits(y1);
+                    }
                 }
             }
         }
@@ -264,65 +334,43 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(
     }
 }
 
-template <int ROPE, int NORM, int G>
-int dispatch_slots(unsigned grid, unsigned threads, hipStream_t s, float* qo, const float* qi,
-                   float* k, const float* wq, const float* wk, int64_t tokens, int nq, int nkv,
-                   int slots, float eps, const int32_t* positions, int pos0, const InvFreq& tab) {
+template <int ROPE, int NORM, int G, bool KV>
+int dispatch_slots(unsigned grid, unsigned threads, hipStream_t s, const HeadArgs& a, int slots,
+                   const InvFreq& tab) {
     if (slots == 1)
-        return launch(head_ops_vec_kernel<ROPE, NORM, G, 1>, dim3(grid), dim3(threads), 0, s, qo, qi,
-                      k, wq, wk, tokens, nq, nkv, eps, positions, pos0, tab);
-    return launch(head_ops_vec_kernel<ROPE, NORM, G, 2>, dim3(grid), dim3(threads), 0, s, qo, qi, k,
-                  wq, wk, tokens, nq, nkv, eps, positions, pos0, tab);
+        return launch(head_ops_vec_kernel<ROPE, NORM, G, 1, KV>, dim3(grid), dim3(threads), 0, s, a, tab);
+    return launch(head_ops_vec_kernel<ROPE, NORM, G, 2, KV>, dim3(grid), dim3(threads), 0, s, a, tab);
 }
 
-template <int ROPE, int NORM>
-int dispatch_vec(int G, unsigned grid, unsigned threads, hipStream_t s, float* qo, const float* qi,
-                 float* k, const float* wq, const float* wk, int64_t tokens, int nq, int nkv,
-                 int slots, float eps, const int32_t* positions, int pos0, const InvFreq& tab) {
+template <int ROPE, int NORM, bool KV>
+int dispatch_vec(int G, unsigned grid, unsigned threads, hipStream_t s, const HeadArgs& a, int slots,
+                 const InvFreq& tab) {
     switch (G) {
-        case 8:
-            return dispatch_slots<ROPE, NORM, 8>(grid, threads, s, qo, qi, k, wq, wk, tokens, nq, nkv,
-                                                 slots, eps, positions, pos0, tab);
-        case 16:
-            return dispatch_slots<ROPE, NORM, 16>(grid, threads, s, qo, qi, k, wq, wk, tokens, nq,
-                                                  nkv, slots, eps, positions, pos0, tab);
-        case 32:
-            return dispatch_slots<ROPE, NORM, 32>(grid, threads, s, qo, qi, k, wq, wk, tokens, nq,
-                                                  nkv, slots, eps, positions, pos0, tab);
-        default:
-            return FENCE_ERROR_INVALID_VALUE;
+        case 8: return dispatch_slots<ROPE, NORM, 8, KV>(grid, threads, s, a, slots, tab);
+        case 16: return dispatch_slots<ROPE, NORM, 16, KV>(grid, threads, s, a, slots, tab);
+        case 32: return dispatch_slots<ROPE, NORM, 32, KV>(grid, threads, s, a, slots, tab);
+        default: return FENCE_ERROR_INVALID_VALUE;
     }
 }
 
 template <int ROPE, int NORM>
-int dispatch(bool vec, int G, unsigned grid, unsigned threads, hipStream_t s, float* qo,
-             const float* qi, float* k, const float* wq, const float* wk, int64_t tokens, int nq,
-             int nkv, int hd, int slots, float eps, const int32_t* positions, int pos0,
-             const InvFreq& tab) {
-    if (vec)
-        return dispatch_vec<ROPE, NORM>(G, grid, threads, s, qo, qi, k, wq, wk, tokens, nq, nkv,
-                                        slots, eps, positions, pos0, tab);
-    return launch(head_ops_scalar_kernel<ROPE, NORM>, dim3(grid), dim3(256), 0, s, qo, qi, k, wq,
-                  wk, tokens, nq, nkv, hd, eps, positions, pos0, tab);
+int dispatch(bool vec, int G, unsigned grid, unsigned threads, hipStream_t s, const HeadArgs& a, int hd,
+             int slots, const InvFreq& tab) {
+    if (!vec) return launch(head_ops_scalar_kernel<ROPE, NORM>, dim3(grid), dim3(256), 0, s, a, hd, tab);
+    if constexpr (ROPE != kRopeNone && NORM != kNormRow) {  // the KV store follows a RoPE
+        if (a.kc) return dispatch_vec<ROPE, NORM, true>(G, grid, threads, s, a, slots, tab);
+    }
+    return dispatch_vec<ROPE, NORM, false>(G, grid, threads, s, a, slots, tab);
 }
 
 template <int ROPE>
-int dispatch_norm(int norm, bool vec, int G, unsigned grid, unsigned threads, hipStream_t s,
-                  float* qo, const float* qi, float* k, const float* wq, const float* wk,
-                  int64_t tokens, int nq, int nkv, int hd, int slots, float eps,
-                  const int32_t* positions, int pos0, const InvFreq& tab) {
+int dispatch_norm(int norm, bool vec, int G, unsigned grid, unsigned threads, hipStream_t s, const HeadArgs& a,
+                  int hd, int slots, const InvFreq& tab) {
     switch (norm) {
-        case kNormNone:
-            return dispatch<ROPE, kNormNone>(vec, G, grid, threads, s, qo, qi, k, wq, wk, tokens,
-                                             nq, nkv, hd, slots, eps, positions, pos0, tab);
-        case kNormRow:
-            return dispatch<ROPE, kNormRow>(vec, G, grid, threads, s, qo, qi, k, wq, wk, tokens, nq,
-                                            nkv, hd, slots, eps, positions, pos0, tab);
-        case kNormHead:
-            return dispatch<ROPE, kNormHead>(vec, G, grid, threads, s, qo, qi, k, wq, wk, tokens,
-                                             nq, nkv, hd, slots, eps, positions, pos0, tab);
-        default:
-            return FENCE_ERROR_INVALID_VALUE;
+        case kNormNone: return dispatch<ROPE, kNormNone>(vec, G, grid, threads, s, a, hd, slots, tab);
+        case kNormRow: return dispatch<ROPE, kNormRow>(vec, G, grid, threads, s, a, hd, slots, tab);
+        case kNormHead: return dispatch<ROPE, kNormHead>(vec, G, grid, threads, s, a, hd, slots, tab);
+        default: return FENCE_ERROR_INVALID_VALUE;
     }
 }
 
@@ -352,9 +400,12 @@ void rope_inv_freq_host(float* out, int hd, float base) {
 //   qo/qi: q output/input [tokens][nq][hd] (equal for the in-place forms)
 //   k:     [tokens][nkv][hd], in place
 //   norm:  none | row (q row, weight wq[nq*hd]) | head (wq[hd], wk[hd])
+//   kv:    optional KV store (kc, vc, v, max_ctx; see HeadArgs), with a RoPE
+//          and without the row norm
 int head_ops_launch(float* qo, const float* qi, float* k, const float* wq, const float* wk,
                     int64_t tokens, int nq, int nkv, int hd, float eps, const int32_t* positions,
-                    int pos0, float base, int rope, int norm, hipStream_t s) {
+                    int pos0, float base, int rope, int norm, hipStream_t s, uint16_t* kc = nullptr,
+                    uint16_t* vc = nullptr, const float* v = nullptr, int max_ctx = 0) {
     if (tokens < 0 || nq < 0 || nkv < 0 || hd <= 0) return FENCE_ERROR_INVALID_VALUE;
     if (rope != kRopeNone && rope != kRopeNeox && rope != kRopeInter) return FENCE_ERROR_INVALID_VALUE;
     if (nq > 0 && (!qo || !qi)) return FENCE_ERROR_INVALID_VALUE;
@@ -367,6 +418,12 @@ int head_ops_launch(float* qo, const float* qi, float* k, const float* wq, const
     }
     if (!ok4(qo) || !ok4(qi) || !ok4(k) || !ok4(wq) || !ok4(wk) || !ok4(positions))
         return FENCE_ERROR_INVALID_VALUE;
+    if (kc) {
+        if (!vc || !v || nkv <= 0 || max_ctx <= 0 || rope == kRopeNone || norm == kNormRow) return FENCE_ERROR_INVALID_VALUE;
+        if (!aligned(kc, 2) || !aligned(vc, 2) || !ok4(v)) return FENCE_ERROR_INVALID_VALUE;
+        // positions from pos0 are checked here; device positions by the kernel
+        if (!positions && (pos0 < 0 || static_cast<int64_t>(pos0) + tokens > max_ctx)) return FENCE_ERROR_INVALID_VALUE;
+    }
     if (tokens == 0 || nq + nkv == 0) return FENCE_SUCCESS;
     if (nq == 0) {  // keep q pointers valid for address arithmetic only
         qo = k;
@@ -379,21 +436,16 @@ int head_ops_launch(float* qo, const float* qi, float* k, const float* wq, const
 
     const int G = hd / 8;
     bool vec = (hd == 64 || hd == 128 || hd == 256) && ok16(qo) && ok16(qi) && ok16(k) &&
-               ok16(wq) && ok16(wk);
+               ok16(wq) && ok16(wk) && ok16(kc) && ok16(vc) && ok16(v);
     unsigned threads = 256;
     int slots = 0;
     if (vec) vec = plan_row(tokens, static_cast<int64_t>(nq + nkv) * G, FENCE_HEAD_SLOTS, 2, &threads, &slots);
     const unsigned grid = grid_1d(tokens, 1, 1 << 20);
+    const HeadArgs a{qo, qi, k, wq, wk, tokens, nq, nkv, eps, positions, pos0, kc, vc, v, max_ctx};
     switch (rope) {
-        case kRopeNone:
-            return dispatch_norm<kRopeNone>(norm, vec, G, grid, threads, s, qo, qi, k, wq, wk,
-                                            tokens, nq, nkv, hd, slots, eps, positions, pos0, tab);
-        case kRopeNeox:
-            return dispatch_norm<kRopeNeox>(norm, vec, G, grid, threads, s, qo, qi, k, wq, wk,
-                                            tokens, nq, nkv, hd, slots, eps, positions, pos0, tab);
-        default:
-            return dispatch_norm<kRopeInter>(norm, vec, G, grid, threads, s, qo, qi, k, wq, wk,
-                                             tokens, nq, nkv, hd, slots, eps, positions, pos0, tab);
+        case kRopeNone: return dispatch_norm<kRopeNone>(norm, vec, G, grid, threads, s, a, hd, slots, tab);
+        case kRopeNeox: return dispatch_norm<kRopeNeox>(norm, vec, G, grid, threads, s, a, hd, slots, tab);
+        default: return dispatch_norm<kRopeInter>(norm, vec, G, grid, threads, s, a, hd, slots, tab);
     }
 }
 
@@ -429,6 +481,18 @@ extern "C" int fence_qk_norm_rope(float* q, float* k, const float* q_norm_w, con
     if (style != FENCE_ROPE_NEOX && style != FENCE_ROPE_INTERLEAVED) return FENCE_ERROR_INVALID_VALUE;
     return head_ops_launch(q, q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads, head_dim,
                            eps, positions, pos0, freq_base, style, fence::kNormHead, stream);
+}
+
+extern "C" int fence_qk_norm_rope_store_kv(float* q, float* k, const float* v, const float* q_norm_w,
+                                           const float* k_norm_w, void* k_cache, void* v_cache, int max_ctx,
+                                           int64_t tokens, int n_q_heads, int n_kv_heads, int head_dim,
+                                           float eps, const int32_t* positions, int pos0, float freq_base,
+                                           int style, hipStream_t stream) {
+    if (style != FENCE_ROPE_NEOX && style != FENCE_ROPE_INTERLEAVED) return FENCE_ERROR_INVALID_VALUE;
+    if (!k_cache || (q_norm_w == nullptr) != (k_norm_w == nullptr)) return FENCE_ERROR_INVALID_VALUE;
+    return head_ops_launch(q, q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads, head_dim, eps, positions,
+                           pos0, freq_base, style, q_norm_w ? fence::kNormHead : fence::kNormNone, stream,
+                           static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), v, max_ctx);
 }
 
 extern "C" int fence_rms_norm_rope(float* out, const float* x, const float* w, float* k,

@@ -312,7 +312,7 @@ bool Qwen3Model::load(const std::string& gguf_path, int max_ctx, hipStream_t str
     const size_t f32_sizes[] = {E, E, E, Q, KV, KV, Q, FF, FF, E, size_t(c.vocab_size), size_t(c.n_heads) * max_ctx};
     size_t total = 0;
     for (size_t n : f32_sizes) total += align_up(n * 4, kAlign);
-    total += align_up(half_n * 2, kAlign) + kAlign;
+    total += align_up(half_n * 2, kAlign) + align_up(FF * 2, kAlign) + kAlign;
     if (hipMalloc(&scratch_arena_, total) != hipSuccess || hipHostMalloc(&host_token_, sizeof(int)) != hipSuccess) {
         unload();
         return fail("out of memory for scratch buffers", FENCE_ERROR_OUT_OF_MEMORY);
@@ -337,6 +337,7 @@ bool Qwen3Model::load(const std::string& gguf_path, int max_ctx, hipStream_t str
     s.logits = reinterpret_cast<float*>(take(size_t(c.vocab_size) * 4));
     s.score_buf = reinterpret_cast<float*>(take(size_t(c.n_heads) * max_ctx * 4));
     s.x_half = reinterpret_cast<__half*>(take(half_n * 2));
+    s.act_half = reinterpret_cast<__half*>(take(FF * 2));
     s.argmax_out = reinterpret_cast<int*>(take(sizeof(int)));
     hipError_t e = hipMemsetAsync(kv_arena_, 0, per_cache * 2 * c.n_layers, stream_);
     if (e == hipSuccess) e = hipStreamSynchronize(stream_);
@@ -420,8 +421,12 @@ bool Qwen3Model::forward_reference(int token_id, int pos) {
 // The same step with the sub-block outputs kept apart from the residual
 // stream: each projection back to embed_dim (o, down) writes `down`, and the
 // next RMSNorm adds it into `hidden` in the same pass (hidden + down is the
-// reference's residual_add(hidden = o, residual), the same sum).  15 launches
-// per layer instead of 22 plus two copies.
+// reference's residual_add(hidden = o, residual), the same sum).  q, k and v
+// are one launch; QK-norm, RoPE and the KV store another; attention writes
+// the binary16 input of the o projection itself; gate, up and SwiGLU are one
+// launch (writing act_half, since x_half is still being read).  9 calls per
+// layer instead of 22 plus two copies; every result is bit-identical to the
+// reference sequence's.
 bool Qwen3Model::forward_fused(int token_id, int pos) {
     const Qwen3Config& c = config;
     ScratchBuffers& s = scratch;
@@ -432,28 +437,22 @@ bool Qwen3Model::forward_fused(int token_id, int pos) {
     for (int l = 0; l < c.n_layers; ++l) {
         const Qwen3LayerWeights& w = weights.layers[l];
         FENCE_STEP(fence_residual_rms_norm_f16(s.hidden, pending, w.attn_norm, nullptr, s.x_half, 1, E, c.rms_eps, st));
-        FENCE_STEP(w.attn_q_bias ? fence_gemv_q6k_bias(w.attn_q, s.x_half, w.attn_q_bias, s.q, c.q_dim(), E, st)
-                                 : fence_gemv_q6k(w.attn_q, s.x_half, s.q, c.q_dim(), E, st));
-        FENCE_STEP(w.attn_k_bias ? fence_gemv_q6k_bias(w.attn_k, s.x_half, w.attn_k_bias, s.k, c.kv_dim(), E, st)
-                                 : fence_gemv_q6k(w.attn_k, s.x_half, s.k, c.kv_dim(), E, st));
-        FENCE_STEP(w.attn_v_bias ? fence_gemv_q6k_bias(w.attn_v, s.x_half, w.attn_v_bias, s.v, c.kv_dim(), E, st)
-                                 : fence_gemv_q6k(w.attn_v, s.x_half, s.v, c.kv_dim(), E, st));
-        if (w.attn_q_norm && w.attn_k_norm)
-            FENCE_STEP(fence_qk_norm_rope(s.q, s.k, w.attn_q_norm, w.attn_k_norm, 1, c.n_heads, c.n_kv_heads,
-                                          c.head_dim, c.rms_eps, nullptr, pos, c.rope_freq_base, FENCE_ROPE_NEOX, st));
-        else
-            FENCE_STEP(fence_rope(s.q, s.k, 1, c.n_heads, c.n_kv_heads, c.head_dim, nullptr, pos, c.rope_freq_base,
-                                  FENCE_ROPE_NEOX, st));
-        FENCE_STEP(fence_store_kv(kv_cache.k[l], kv_cache.v[l], s.k, s.v, pos, c.kv_dim(), c.max_ctx, st));
-        FENCE_STEP(fence_gqa_attention(s.attn_out, s.q, kv_cache.k[l], kv_cache.v[l], c.head_dim, c.n_heads,
-                                       c.n_kv_heads, pos + 1, c.max_ctx, s.score_buf, st));
-        FENCE_STEP(fence_f32_to_f16(s.x_half, s.attn_out, c.q_dim(), st));
+        const void* w_qkv[3] = {w.attn_q, w.attn_k, w.attn_v};
+        float* y_qkv[3] = {s.q, s.k, s.v};
+        const float* b_qkv[3] = {w.attn_q_bias, w.attn_k_bias, w.attn_v_bias};
+        const int m_qkv[3] = {c.q_dim(), c.kv_dim(), c.kv_dim()};
+        FENCE_STEP(fence_gemv_q6k_multi(3, w_qkv, y_qkv, b_qkv, m_qkv, s.x_half, E, st));
+        const bool qk_norm = w.attn_q_norm && w.attn_k_norm;
+        FENCE_STEP(fence_qk_norm_rope_store_kv(s.q, s.k, s.v, qk_norm ? w.attn_q_norm : nullptr,
+                                               qk_norm ? w.attn_k_norm : nullptr, kv_cache.k[l], kv_cache.v[l],
+                                               c.max_ctx, 1, c.n_heads, c.n_kv_heads, c.head_dim, c.rms_eps, nullptr,
+                                               pos, c.rope_freq_base, FENCE_ROPE_NEOX, st));
+        FENCE_STEP(fence_gqa_attention_f16(nullptr, s.x_half, s.q, kv_cache.k[l], kv_cache.v[l], c.head_dim,
+                                           c.n_heads, c.n_kv_heads, pos + 1, c.max_ctx, s.score_buf, st));
         FENCE_STEP(fence_gemv_q6k(w.attn_output, s.x_half, s.down, E, c.q_dim(), st));
         FENCE_STEP(fence_residual_rms_norm_f16(s.hidden, s.down, w.ffn_norm, nullptr, s.x_half, 1, E, c.rms_eps, st));
-        FENCE_STEP(fence_gemv_q6k(w.ffn_gate, s.x_half, s.gate, c.ff_dim, E, st));
-        FENCE_STEP(fence_gemv_q6k(w.ffn_up, s.x_half, s.up, c.ff_dim, E, st));
-        FENCE_STEP(fence_swiglu_f16(s.x_half, nullptr, s.gate, s.up, c.ff_dim, st));
-        FENCE_STEP(fence_gemv_q6k(w.ffn_down, s.x_half, s.down, E, c.ff_dim, st));
+        FENCE_STEP(fence_gemv_q6k_swiglu_f16(w.ffn_gate, w.ffn_up, s.x_half, s.act_half, nullptr, c.ff_dim, E, st));
+        FENCE_STEP(fence_gemv_q6k(w.ffn_down, s.act_half, s.down, E, c.ff_dim, st));
         pending = s.down;
     }
     FENCE_STEP(fence_residual_rms_norm_f16(s.hidden, pending, weights.output_norm, s.normed, nullptr, 1, E, c.rms_eps, st));

@@ -18,10 +18,6 @@ namespace {
 constexpr int kSwigluThreads = 256;
 constexpr int kSwigluUnroll = 1;
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    return (g / (1.0f + expf(-g))) * u;
-}
-
 // OUT32: fp32 result to `out`; OUT16: its binary16 rounding to `out16`
 // (the f32_to_f16 that src/model/qwen3.cu:336 runs as a separate pass).
 template <int UNROLL, bool OUT32, bool OUT16>

@@ -48,9 +48,13 @@ SIGNATURES = {
     "fence_f16_to_f32": (_P, _P, _I, _P),
     "fence_residual_rms_norm_f16": (_P, _P, _P, _P, _P, _L, _I, _F, _P),
     "fence_swiglu_f16": (_P, _P, _P, _P, _L, _P),
+    "fence_gemv_q6k_multi": (_I, _P, _P, _P, _P, _P, _I, _P),
+    "fence_gemv_q6k_swiglu_f16": (_P, _P, _P, _P, _P, _I, _I, _P),
     "fence_rms_norm_rows": (_P, _P, _P, _L, _I, _F, _P),
     "fence_rope": (_P, _P, _L, _I, _I, _I, _P, _I, _F, _I, _P),
     "fence_qk_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
+    "fence_gqa_attention_f16": (_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P),
+    "fence_qk_norm_rope_store_kv": (_P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_rms_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_swiglu": (_P, _P, _P, _L, _P),
     "fence_softmax_rows": (_P, _L, _I, _L, _P),
@@ -190,6 +194,18 @@ def swiglu_f16(out_f16, out, gate, up, n, stream=None):
     _call("fence_swiglu_f16", out_f16, out, gate, up, n, stream)
 
 
+def gemv_q6k_multi(Ws, x, ys, Ms, K, biases=None, stream=None):
+    """Ws, ys, Ms (and biases, entries may be None): lists of n <= 4 entries."""
+    n = len(Ws)
+    arr = lambda vals: (ctypes.c_void_p * n)(*vals)  # noqa: E731
+    _call("fence_gemv_q6k_multi", n, arr(Ws), arr(ys), None if biases is None else arr(biases),
+          (ctypes.c_int * n)(*Ms), x, K, stream)
+
+
+def gemv_q6k_swiglu_f16(W_gate, W_up, x, out_f16, out, M, K, stream=None):
+    _call("fence_gemv_q6k_swiglu_f16", W_gate, W_up, x, out_f16, out, M, K, stream)
+
+
 def rms_norm_rows(out, x, w, rows, n, eps, stream=None):
     _call("fence_rms_norm_rows", out, x, w, rows, n, eps, stream)
 
@@ -204,6 +220,18 @@ def qk_norm_rope(q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads, head_d
                  positions, pos0, freq_base, style, stream=None):
     _call("fence_qk_norm_rope", q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads,
           head_dim, eps, positions, pos0, freq_base, style, stream)
+
+
+def gqa_attention_f16(attn_out, out_f16, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, seq_len, max_ctx,
+                      score_buf, stream=None):
+    _call("fence_gqa_attention_f16", attn_out, out_f16, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads,
+          seq_len, max_ctx, score_buf, stream)
+
+
+def qk_norm_rope_store_kv(q, k, v, wq, wk, k_cache, v_cache, max_ctx, tokens, n_q_heads, n_kv_heads, head_dim,
+                          eps, positions, pos0, freq_base, style, stream=None):
+    _call("fence_qk_norm_rope_store_kv", q, k, v, wq, wk, k_cache, v_cache, max_ctx, tokens, n_q_heads,
+          n_kv_heads, head_dim, eps, positions, pos0, freq_base, style, stream)
 
 
 def rms_norm_rope(out, x, w, k, tokens, n_q_heads, n_kv_heads, head_dim, eps, positions, pos0,

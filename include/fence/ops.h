@@ -193,6 +193,33 @@ int fence_qk_norm_rope(float* q, float* k, const float* q_norm_w,
                        const int32_t* positions, int pos0, float freq_base,
                        int style, hipStream_t stream);
 
+/* fence_gqa_attention with its conversion for the o projection
+ * (src/model/qwen3.cu:304-308: gqa_attention, then f32_to_f16 of attn_out)
+ * in the same launches: out_f16 [n_q_heads][head_dim] = binary16 of the
+ * result, bit-identical to the two calls; attn_out (fp32) may be NULL. */
+int fence_gqa_attention_f16(float* attn_out, void* out_f16, const float* q,
+                            const void* k_cache, const void* v_cache, int head_dim,
+                            int n_q_heads, int n_kv_heads, int seq_len, int max_ctx,
+                            float* score_buf, hipStream_t stream);
+
+/* fence_qk_norm_rope, then store_kv of the rotated k and of v, in one pass
+ * (src/model/qwen3.cu:293-300): after the norm and RoPE of token t's q and k
+ * (both still written in fp32), its k and v [n_kv_heads*head_dim] are
+ * written as binary16 into row pos_t of k_cache / v_cache
+ * [max_ctx][n_kv_heads*head_dim] (store_kv, src/kernels/ops.cuh:419-443),
+ * bit-identical to the separate calls.  v: [tokens][n_kv_heads][head_dim].
+ * q_norm_w and k_norm_w both NULL: RoPE only (the reference skips QK-norm
+ * when a model has no norm weights, src/model/qwen3.cu:293).  Positions from
+ * pos0 must lie in [0, max_ctx); a device position outside it stores
+ * nothing. */
+int fence_qk_norm_rope_store_kv(float* q, float* k, const float* v,
+                                const float* q_norm_w, const float* k_norm_w,
+                                void* k_cache, void* v_cache, int max_ctx,
+                                int64_t tokens, int n_q_heads, int n_kv_heads,
+                                int head_dim, float eps, const int32_t* positions,
+                                int pos0, float freq_base, int style,
+                                hipStream_t stream);
+
 /* out_t = RoPE(rms_norm(x_t, w)) for x [tokens][n_q_heads*head_dim],
  * w [n_q_heads*head_dim], the normalised row viewed as n_q_heads heads; k
  * (may be NULL) gets RoPE only.  out may equal x. */
@@ -253,6 +280,23 @@ int fence_residual_rms_norm_f16(float* hidden, const float* residual, const floa
  * be NULL. */
 int fence_swiglu_f16(void* out_f16, float* out, const float* gate, const float* up,
                      int64_t n, hipStream_t stream);
+
+/* Several Q6_K GEMVs that share x and K in one launch: y[i] = W[i] x
+ * (+ bias[i]) for i < n <= 4 -- the q, k and v projections of
+ * src/model/qwen3.cu:281-289 as one launch.  W, y and M are host arrays of n
+ * entries; bias is NULL or a host array whose entries may be NULL.  Each y[i]
+ * is bit-identical to fence_gemv_q6k(_bias) on the same operands. */
+int fence_gemv_q6k_multi(int n, const void* const* W, float* const* y,
+                         const float* const* bias, const int* M, const void* x,
+                         int K, hipStream_t stream);
+
+/* The gate and up projections with SwiGLU and its conversion
+ * (src/model/qwen3.cu:328-336) in one launch: act[r] = silu(W_gate[r] . x) *
+ * (W_up[r] . x); out_f16 = binary16(act); out (fp32 act) may be NULL.
+ * Bit-identical to fence_gemv_q6k on each matrix, then fence_swiglu_f16. */
+int fence_gemv_q6k_swiglu_f16(const void* W_gate, const void* W_up, const void* x,
+                              void* out_f16, float* out, int M, int K,
+                              hipStream_t stream);
 
 int fence_rope_inv_freq(float* inv_freq, int head_dim, float freq_base);
 

@@ -98,11 +98,13 @@ struct ScratchBuffers {
     float* score_buf = nullptr;  // [n_heads * max_ctx]
     __half* x_half = nullptr;    // [max(embed_dim, ff_dim, q_dim)]
     int* argmax_out = nullptr;   // [1]
+    __half* act_half = nullptr;  // [ff_dim]: SwiGLU output of the fused sequence
 };
 
 /* The kernel sequence forward() launches. */
 enum class Qwen3Sequence {
-    Fused,      // fused epilogues and QK-norm + RoPE: 15 launches per layer
+    Fused,      // fused epilogues, q/k/v, QK-norm + RoPE + KV store, attention + conversion,
+                // gate/up + SwiGLU: 9 calls per layer
     Reference,  // the reference's launcher order, src/model/qwen3.cu:267-341
 };
 

@@ -99,6 +99,25 @@ def _raw(name):
     ("fence_gemv_q6k", (0x1001, 32, 48, 8, 256, None)),           # W not 2-byte aligned
     ("fence_gemv_q6k", (16, 32, 48, 8, 0, None)),                 # K == 0
     ("fence_gemv_q6k_bias", (16, 32, None, 48, 8, 256, None)),    # bias missing
+    ("fence_gqa_attention_f16", (16, None, 32, 48, 64, 128, 8, 2, 10, 100, 80, None)),  # out_f16 missing
+    ("fence_gqa_attention_f16", (None, 0x1001, 32, 48, 64, 128, 8, 2, 10, 100, 80, None)),  # misaligned
+    ("fence_qk_norm_rope_store_kv", (16, 32, 48, 64, 80, None, 96, 100, 1, 4, 2, 128, 1e-6, None, 0, 1e6, 0,
+                                     None)),                        # k_cache missing
+    ("fence_qk_norm_rope_store_kv", (16, 32, 48, 64, None, 96, 112, 100, 1, 4, 2, 128, 1e-6, None, 0, 1e6, 0,
+                                     None)),                        # one norm weight only
+    ("fence_qk_norm_rope_store_kv", (16, 32, None, 64, 80, 96, 112, 100, 1, 4, 2, 128, 1e-6, None, 0, 1e6, 0,
+                                     None)),                        # v missing
+    ("fence_qk_norm_rope_store_kv", (16, 32, 48, 64, 80, 96, 112, 100, 1, 4, 2, 128, 1e-6, None, 100, 1e6, 0,
+                                     None)),                        # position past max_ctx
+    ("fence_qk_norm_rope_store_kv", (16, 32, 48, 64, 80, 96, 112, 100, 1, 4, 2, 128, 1e-6, None, 0, 1e6, 5,
+                                     None)),                        # bad style
+    ("fence_gemv_q6k_multi", (0, 16, 32, None, 48, 64, 256, None)),   # no matrices
+    ("fence_gemv_q6k_multi", (5, 16, 32, None, 48, 64, 256, None)),   # more than four
+    ("fence_gemv_q6k_multi", (2, None, 32, None, 48, 64, 256, None)),  # W array missing
+    ("fence_gemv_q6k_swiglu_f16", (16, 32, 48, 64, None, 8, 300, None)),  # K % 256 != 0
+    ("fence_gemv_q6k_swiglu_f16", (16, 32, 48, 64, None, -1, 256, None)),
+    ("fence_gemv_q6k_swiglu_f16", (16, 32, 48, None, None, 8, 256, None)),  # out_f16 missing
+    ("fence_gemv_q6k_swiglu_f16", (16, 0x1001, 48, 64, None, 8, 256, None)),  # W_up misaligned
     ("fence_gqa_attention", (16, 32, 48, 64, 128, 6, 4, 10, 100, 80, None)),   # 6 % 4 != 0
     ("fence_gqa_attention", (16, 32, 48, 64, 128, 8, 2, 101, 100, 80, None)),  # seq_len > max_ctx
     ("fence_store_kv", (16, 32, 48, 64, 100, 512, 100, None)),                # pos == max_ctx

@@ -1,0 +1,134 @@
+"""GPU checks of the decode-step fusions that replace two reference launches
+with one: fence_gqa_attention_f16 (gqa_attention + f32_to_f16,
+src/model/qwen3.cu:304-308) and fence_qk_norm_rope_store_kv
+(rms_norm_per_head x2 + apply_rope + store_kv, src/model/qwen3.cu:293-302).
+
+The bar is bit equality with the separate entry points on the same operands
+(each of which has its own oracle parity tests); one case per function is
+also checked against the oracle directly.
+"""
+import numpy as np
+import pytest
+
+import fence_ops as F
+from gpu_util import LIVE, dev, host, stream, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+
+def caches(rng, ctx, kv_dim):
+    return (rng.standard_normal((ctx, kv_dim)).astype(np.float16).view(np.uint16),
+            rng.standard_normal((ctx, kv_dim)).astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("hd,n_q,n_kv,seq,ctx", [
+    (128, 32, 8, 1, 4096), (128, 32, 8, 100, 4096), (128, 32, 8, 2916, 4096), (128, 32, 8, 4096, 4096),
+    (128, 8, 8, 300, 512), (64, 16, 4, 333, 512), (96, 16, 4, 333, 512)])
+@pytest.mark.parametrize("with_fp32", [True, False])
+def test_attention_f16_equals_attention_then_conversion(oracle, hd, n_q, n_kv, seq, ctx, with_fp32):
+    torch = torch_mod()
+    rng = np.random.default_rng(seq + hd)
+    kc, vc = caches(rng, ctx, n_kv * hd)
+    q = (rng.standard_normal(n_q * hd) * 0.3).astype(np.float32)
+    qd, kd, vd = dev(q), dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    ws = torch.empty(n_q * ctx, dtype=torch.float32, device="cuda")
+    ref32 = torch.empty(n_q * hd, dtype=torch.float32, device="cuda")
+    ref16 = torch.empty(n_q * hd, dtype=torch.int16, device="cuda")
+    got32 = torch.full((n_q * hd,), float("nan"), dtype=torch.float32, device="cuda")
+    got16 = torch.full((n_q * hd,), -1, dtype=torch.int16, device="cuda")
+    LIVE.extend([ws, ref32, ref16, got32, got16])
+    F.gqa_attention(ref32.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), hd, n_q, n_kv, seq, ctx,
+                    ws.data_ptr(), stream())
+    F.f32_to_f16(ref16.data_ptr(), ref32.data_ptr(), n_q * hd, stream())
+    F.gqa_attention_f16(got32.data_ptr() if with_fp32 else None, got16.data_ptr(), qd.data_ptr(), kd.data_ptr(),
+                        vd.data_ptr(), hd, n_q, n_kv, seq, ctx, ws.data_ptr(), stream())
+    assert np.array_equal(host(got16), host(ref16))
+    if with_fp32:
+        assert np.array_equal(host(got32).view(np.uint32), host(ref32).view(np.uint32))
+    if seq == 100 and hd == 128:
+        r = oracle.f32_to_f16(oracle.gqa_attention(q, kc, vc, n_q, n_kv, hd, seq))
+        diff = np.abs(host(got16).view(np.float16).astype(np.float64) - r.view(np.float16).astype(np.float64))
+        assert np.max(diff) <= 2.0 ** -10 * np.max(np.abs(r.view(np.float16).astype(np.float64)))
+
+
+def run_fused_kv(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, pos0, base, style, offset=0):
+    torch = torch_mod()
+    ctx = kc.shape[0]
+    qd, kd, vdv = dev(q), dev(k), dev(v)
+    kcd, vcd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    pd = None if positions is None else dev(np.asarray(positions, np.int32))
+    F.qk_norm_rope_store_kv(qd.data_ptr(), kd.data_ptr(), vdv.data_ptr(),
+                            None if wq is None else dev(wq).data_ptr(), None if wk is None else dev(wk).data_ptr(),
+                            kcd.data_ptr(), vcd.data_ptr(), ctx, T, nq, nkv, hd, 1e-6,
+                            None if pd is None else pd.data_ptr(), pos0, base, style, stream())
+    return host(qd), host(kd), host(kcd).view(np.uint16), host(vcd).view(np.uint16)
+
+
+def run_separate(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, pos0, base, style):
+    """qk_norm_rope (or rope) then store_kv per token, the reference's order."""
+    ctx = kc.shape[0]
+    qd, kd, vdv = dev(q), dev(k), dev(v)
+    kcd, vcd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    pd = None if positions is None else dev(np.asarray(positions, np.int32))
+    pp = None if pd is None else pd.data_ptr()
+    if wq is None:
+        F.rope(qd.data_ptr(), kd.data_ptr(), T, nq, nkv, hd, pp, pos0, base, style, stream())
+    else:
+        F.qk_norm_rope(qd.data_ptr(), kd.data_ptr(), dev(wq).data_ptr(), dev(wk).data_ptr(), T, nq, nkv, hd, 1e-6,
+                       pp, pos0, base, style, stream())
+    kv = nkv * hd
+    for t in range(T):
+        pos = positions[t] if positions is not None else pos0 + t
+        if 0 <= pos < ctx:
+            F.store_kv(kcd.data_ptr(), vcd.data_ptr(), kd.data_ptr() + 4 * t * kv, vdv.data_ptr() + 4 * t * kv, pos,
+                       kv, ctx, stream())
+    return host(qd), host(kd), host(kcd).view(np.uint16), host(vcd).view(np.uint16)
+
+
+@pytest.mark.parametrize("T,nq,nkv,hd,norm,style,pos0", [
+    (1, 32, 8, 128, True, F.ROPE_NEOX, 2915),     # Qwen3-4B decode step
+    (1, 32, 8, 128, False, F.ROPE_NEOX, 17),      # no QK-norm weights: RoPE only
+    (1, 64, 8, 128, True, F.ROPE_NEOX, 4095),     # last position; two slots per lane
+    (5, 16, 4, 128, True, F.ROPE_INTERLEAVED, 40),
+    (3, 8, 2, 64, True, F.ROPE_NEOX, 0),
+    (2, 12, 4, 96, True, F.ROPE_NEOX, 9),         # head_dim 96: the scalar kernel
+])
+def test_qk_norm_rope_store_kv_equals_separate_calls(oracle, T, nq, nkv, hd, norm, style, pos0):
+    rng = np.random.default_rng(T * 1000 + nq + hd)
+    ctx = 4096
+    q = rng.standard_normal((T, nq, hd)).astype(np.float32)
+    k = rng.standard_normal((T, nkv, hd)).astype(np.float32)
+    v = rng.standard_normal((T, nkv, hd)).astype(np.float32)
+    wq = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+    wk = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+    kc, vc = caches(rng, ctx, nkv * hd)
+    got = run_fused_kv(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, None, pos0, 1e6, style)
+    ref = run_separate(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, None, pos0, 1e6, style)
+    for g, r, what in zip(got, ref, ("q", "k", "k cache", "v cache")):
+        assert np.array_equal(g.view(np.uint32 if g.dtype == np.float32 else np.uint16),
+                              r.view(np.uint32 if r.dtype == np.float32 else np.uint16)), what
+    if T == 1 and norm and style == F.ROPE_NEOX:  # and the oracle's store_kv of the oracle's k
+        _, rk = oracle.qk_norm_rope(q, k, wq, wk, 1e-6, None, pos0, 1e6, style)
+        rkc, rvc = oracle.store_kv(kc, vc, rk.reshape(-1), v.reshape(-1), pos0)
+        assert np.array_equal(got[3], rvc)
+        d = np.abs(got[2][pos0].view(np.float16).astype(np.float64) - rkc[pos0].view(np.float16).astype(np.float64))
+        assert np.max(d) <= 2.0 ** -10 * np.max(np.abs(rkc[pos0].view(np.float16).astype(np.float64)))
+        other = np.arange(ctx) != pos0
+        assert np.array_equal(got[2][other], kc[other]) and np.array_equal(got[3][other], vc[other])
+
+
+def test_qk_norm_rope_store_kv_device_positions_skip_out_of_range():
+    """Positions from a device array: one outside [0, max_ctx) stores nothing."""
+    T, nq, nkv, hd, ctx = 4, 16, 4, 128, 64
+    rng = np.random.default_rng(77)
+    q = rng.standard_normal((T, nq, hd)).astype(np.float32)
+    k = rng.standard_normal((T, nkv, hd)).astype(np.float32)
+    v = rng.standard_normal((T, nkv, hd)).astype(np.float32)
+    wq = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    wk = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kc, vc = caches(rng, ctx, nkv * hd)
+    positions = [5, 63, 64, 2]  # 64 is past max_ctx
+    got = run_fused_kv(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, 0, 1e6, F.ROPE_NEOX)
+    ref = run_separate(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, 0, 1e6, F.ROPE_NEOX)
+    assert np.array_equal(got[2], ref[2]) and np.array_equal(got[3], ref[3])
+    assert np.array_equal(got[1].view(np.uint32), ref[1].view(np.uint32))

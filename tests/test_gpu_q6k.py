@@ -164,3 +164,115 @@ def test_gemv_q6k_nan_scale_row(oracle):
     ref = oracle.gemv_q6k(W, x)
     assert np.isnan(ref[3]) and np.isnan(got[3]) and np.isfinite(np.delete(got, 3)).all()
     assert_close(got, ref, np.nan_to_num(abs_scale(W, x, K), nan=0.0), "q6k NaN scale")
+
+
+# ------------------------------------------------- multi-matrix and gate/up + SwiGLU launches
+
+def run_q6k_multi(Ws, x16, Ms, K, biases=None):
+    torch = torch_mod()
+    ys = [torch.full((max(M, 1),), float("nan"), dtype=torch.float32, device="cuda") for M in Ms]
+    LIVE.extend(ys)
+    xd = dev(np.asarray(x16, np.uint16).view(np.int16))
+    wp = [dev(W).data_ptr() if W is not None else None for W in Ws]
+    bp = None if biases is None else [None if b is None else dev(b).data_ptr() for b in biases]
+    F.gemv_q6k_multi(wp, xd.data_ptr(), [y.data_ptr() for y in ys], Ms, K, bp, stream())
+    return [host(y)[:M] for y, M in zip(ys, Ms)]
+
+
+@pytest.mark.parametrize("shapes,K", [
+    ((4096, 1024, 1024), 2560),        # Qwen3-4B q, k, v
+    ((4096, 1024, 1024), 4096),        # Llama-3-8B q, k, v
+    ((512, 256, 256, 8), 5120),        # four matrices, two waves per row
+    ((7, 13, 3), 768),                 # row counts with M * nb % 8 != 0: direct kernel
+    ((64, 0, 32), 2560),               # an empty matrix in the middle
+])
+def test_gemv_q6k_multi_equals_separate_launches(oracle, shapes, K):
+    rng = np.random.default_rng(sum(shapes) + K)
+    Ws = [make_q6k_matrix(rng, M, K) if M else np.zeros((0, K // 256 * 210), np.uint8) for M in shapes]
+    x = rand_x(rng, K)
+    got = run_q6k_multi([W if W.size else None for W in Ws], x, list(shapes), K)
+    for i, (W, M) in enumerate(zip(Ws, shapes)):
+        if M == 0:
+            continue
+        assert np.array_equal(got[i], run_q6k(W, x, M, K)), f"matrix {i}: differs from its own launch"
+        assert_close(got[i], oracle.gemv_q6k(W, x), abs_scale(W, x, K), f"multi {i}")
+
+
+def test_gemv_q6k_multi_biases(oracle):
+    K = 2560
+    rng = np.random.default_rng(21)
+    Ms = (4096, 1024, 1024)
+    Ws = [make_q6k_matrix(rng, M, K) for M in Ms]
+    bs = [rng.standard_normal(M).astype(np.float32) for M in Ms]
+    x = rand_x(rng, K)
+    got = run_q6k_multi(Ws, x, list(Ms), K, [bs[0], None, bs[2]])
+    assert np.array_equal(got[0], run_q6k(Ws[0], x, Ms[0], K, bs[0]))
+    assert np.array_equal(got[1], run_q6k(Ws[1], x, Ms[1], K))
+    assert np.array_equal(got[2], run_q6k(Ws[2], x, Ms[2], K, bs[2]))
+
+
+def run_swiglu(Wg, Wu, x16, M, K, fp32=True):
+    torch = torch_mod()
+    o16 = torch.full((M,), -1, dtype=torch.int16, device="cuda")
+    o32 = torch.full((M,), float("nan"), dtype=torch.float32, device="cuda") if fp32 else None
+    LIVE.extend([o16, o32])
+    F.gemv_q6k_swiglu_f16(dev(Wg).data_ptr(), dev(Wu).data_ptr(), dev(np.asarray(x16, np.uint16).view(np.int16))
+                          .data_ptr(), o16.data_ptr(), o32.data_ptr() if fp32 else None, M, K, stream())
+    return host(o16).view(np.uint16), (host(o32) if fp32 else None)
+
+
+def unfused_swiglu(Wg, Wu, x16, M, K):
+    torch = torch_mod()
+    g = torch.from_numpy(run_q6k(Wg, x16, M, K)).to("cuda")
+    u = torch.from_numpy(run_q6k(Wu, x16, M, K)).to("cuda")
+    o16 = torch.zeros((M,), dtype=torch.int16, device="cuda")
+    o32 = torch.zeros((M,), dtype=torch.float32, device="cuda")
+    LIVE.extend([g, u, o16, o32])
+    F.swiglu_f16(o16.data_ptr(), o32.data_ptr(), g.data_ptr(), u.data_ptr(), M, stream())
+    return host(o16).view(np.uint16), host(o32)
+
+
+@pytest.mark.parametrize("M,K", [
+    (9728, 2560),   # Qwen3-4B gate/up
+    (14336, 4096),  # Llama-3-8B gate/up (16 blocks)
+    (1000, 5120),   # 20 blocks: two waves per row
+    (256, 9728),    # 38 blocks: more than a pair's staging holds -> direct kernel
+    (13, 768),      # M * nb % 8 != 0 -> direct kernel
+    (1, 256),
+    # ~4 rows whose fp32 act rounds onto a binary16 tie: the conversion must
+    # round the fp32 value (as the unfused chain does), not the exact product
+    (65536, 256),
+])
+def test_gemv_q6k_swiglu_equals_unfused_sequence(oracle, M, K):
+    rng = np.random.default_rng(M * 7 + K)
+    Wg, Wu = make_q6k_matrix(rng, M, K), make_q6k_matrix(rng, M, K)
+    x = rand_x(rng, K, std=0.5)
+    got16, got32 = run_swiglu(Wg, Wu, x, M, K)
+    ref16, ref32 = unfused_swiglu(Wg, Wu, x, M, K)
+    assert np.array_equal(got32.view(np.uint32), ref32.view(np.uint32)), "fp32 act differs from the unfused chain"
+    assert np.array_equal(got16, ref16), "binary16 act differs from the unfused chain"
+    assert np.array_equal(run_swiglu(Wg, Wu, x, M, K, fp32=False)[0], ref16)
+    # and against the oracle's chain: act = silu(g) * u with g, u within the GEMV bar
+    g, u = oracle.gemv_q6k(Wg, x), oracle.gemv_q6k(Wu, x)
+    sg, su = abs_scale(Wg, x, K), abs_scale(Wu, x, K)
+    sig = 1 / (1 + np.exp(-g.astype(np.float64)))
+    # d(act) <= |d silu/dg| |u| dg + |silu(g)| du, |d silu/dg| <= 1.1
+    bound = 1.1 * np.abs(u) * GEMV_TOL * sg + np.abs(g * sig) * GEMV_TOL * su + 1e-6 * np.abs(oracle.silu_mul(g, u))
+    assert np.all(np.abs(got32 - oracle.silu_mul(g, u)) <= bound + 1e-30)
+
+
+def test_gemv_q6k_swiglu_unaligned_weights():
+    """W only 2-byte aligned: the direct pair kernel."""
+    torch = torch_mod()
+    M, K = 40, 2560
+    rng = np.random.default_rng(33)
+    Wg, Wu = make_q6k_matrix(rng, M, K), make_q6k_matrix(rng, M, K)
+    x = rand_x(rng, K)
+    raw = torch.zeros(2 * Wg.size + 32, dtype=torch.uint8, device="cuda")
+    o16 = torch.zeros(M, dtype=torch.int16, device="cuda")
+    LIVE.extend([raw, o16])
+    raw[2:2 + Wg.size] = torch.from_numpy(Wg.reshape(-1)).to("cuda")
+    raw[18 + Wg.size:18 + 2 * Wg.size] = torch.from_numpy(Wu.reshape(-1)).to("cuda")
+    F.gemv_q6k_swiglu_f16(raw.data_ptr() + 2, raw.data_ptr() + 18 + Wg.size, dev(x.view(np.int16)).data_ptr(),
+                          o16.data_ptr(), None, M, K, stream())
+    assert np.array_equal(host(o16).view(np.uint16), unfused_swiglu(Wg, Wu, x, M, K)[0])
