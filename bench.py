@@ -20,7 +20,8 @@ recording HIP events at its own kernel start and end
 interval a kernel-trace profiler reports); the roofline of the dominant
 kernel (swiglu) from K such launches;
 the Llama-3-8B decode-step op set in microseconds, the Q8_0 LM-head GEMV
-(128256 x 4096, once per decoded token), a device-copy
+(128256 x 4096, once per decoded token), whole decode steps of a
+Qwen3-4B-shaped model through the GGUF loader and host forward, a device-copy
 calibration, and the CPU baseline (the scalar oracle on one host core,
 timed on a bounded sample of the same step).
 """
@@ -73,6 +74,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--decode-reps", type=int, default=300)
+    ap.add_argument("--decode-tokens", type=int, default=32,
+                    help="tokens of the Qwen3-4B-shaped decode run (0 skips it)")
     ap.add_argument("--lm-head-reps", type=int, default=60,
                     help="launches of the Q8_0 LM-head GEMV pass (0 skips it)")
     ap.add_argument("--all", metavar="PATH", default=None,
@@ -285,12 +288,13 @@ def main():
 
     decode = decode_op_set(torch, F, gen, args.decode_reps)
     lm_head = lm_head_gemv(torch, F, gen, args.lm_head_reps)
+    del sets
+    torch.cuda.empty_cache()
+    decode_model = decode_qwen3_4b(torch, args.decode_tokens)
     copy_gbps = copy_calibration(torch)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     if args.all:
-        del sets
-        torch.cuda.empty_cache()
         all_configs(torch, F, args.all, args.all_reps)
 
     line = {
@@ -318,11 +322,77 @@ def main():
         "roofline": roofline,
         "decode_op_set_llama3_8b": decode,
         "lm_head_gemv_q8_0": lm_head,
+        "decode_qwen3_4b": decode_model,
         "copy_calibration_GBps": copy_gbps,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 4),
     }
     print(json.dumps(line), flush=True)
+
+
+def decode_qwen3_4b(torch, tokens):
+    """Whole decode steps of a Qwen3-4B-shaped model through the GGUF loader
+    and the host forward (include/fence/model.h): a synthetic GGUF file
+    (random weights, the real tensor shapes and types: Q6_K projections, Q8_0
+    tied embedding) is written to shared memory, loaded to HBM, and decoded
+    at positions 2900.. (the KV caches hold zeros there: attention still reads
+    every cached row).  Reported per token: GPU time of `tokens` forwards back
+    to back (the fused sequence and the reference's launch sequence), and the
+    wall time of a greedy loop (forward + argmax + the token read back), as
+    the reference's generate loop runs it (src/model/qwen3.cu:446-501)."""
+    if tokens <= 0:
+        return None
+    import tempfile
+    import fence_model as M
+    import gguf_writer
+    layers, embed, ff, nq, nkv, hd, vocab, pos0 = 36, 2560, 9728, 32, 8, 128, 151936, 2900
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    fd, path = tempfile.mkstemp(suffix=".gguf", dir=d)
+    os.close(fd)
+    try:
+        t0 = time.perf_counter()
+        data_bytes = gguf_writer.synthetic_qwen3(path, seed=11)
+        t1 = time.perf_counter()
+        stream = torch.cuda.current_stream()
+        with M.Model(path, max_ctx=4096, stream=stream.cuda_stream) as m:
+            t2 = time.perf_counter()
+            res = {}
+            for name, seq in (("fused", M.SEQUENCE_FUSED), ("reference_sequence", M.SEQUENCE_REFERENCE)):
+                m.set_sequence(seq)
+                for i in range(3):
+                    m.forward(9707, pos0 + i)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(tokens):
+                    m.forward(9707, pos0 + i)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                res[name] = e0.elapsed_time(e1) * 1e3 / tokens
+            m.set_sequence(M.SEQUENCE_FUSED)
+            tok = 9707
+            w0 = time.perf_counter()
+            for i in range(tokens):
+                tok = m.sample_greedy(m.forward(tok, pos0 + i))
+            greedy_us = (time.perf_counter() - w0) * 1e6 / tokens
+    finally:
+        os.remove(path)
+    q6 = lambda m_, k_: m_ * (k_ // 256) * 210  # noqa: E731
+    weights = layers * (q6(nq * hd, embed) + 2 * q6(nkv * hd, embed) + q6(embed, nq * hd) + 2 * q6(ff, embed)
+                        + q6(embed, ff)) + vocab * (embed // 32) * 34
+    kv = layers * 2 * (pos0 + tokens // 2 + 1) * nkv * hd * 2  # mean attended rows, binary16 K and V
+    per_token = weights + kv
+    return {"model": "Qwen3-4B shapes: 36 layers, embed 2560, ffn 9728, heads 32/8 x 128, vocab 151936; "
+                     "Q6_K projections, Q8_0 tied embedding; synthetic random weights via a GGUF file",
+            "positions": [pos0, pos0 + tokens], "tokens": tokens,
+            "us_per_token_fused": round(res["fused"], 1),
+            "us_per_token_reference_sequence": round(res["reference_sequence"], 1),
+            "tokens_per_s_fused": round(1e6 / res["fused"], 1),
+            "greedy_loop_us_per_token": round(greedy_us, 1),
+            "bytes_per_token": per_token,
+            "GBps_fused": round(per_token / (res["fused"] * 1e-6) / 1e9, 1),
+            "frac_peak_fused": round(per_token / (res["fused"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+            "file_bytes": data_bytes, "write_s": round(t1 - t0, 2), "load_s": round(t2 - t1, 2)}
 
 
 def lm_head_gemv(torch, F, gen, reps):
