@@ -208,44 +208,73 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
     }
 }
 
-// Merge kernel: one workgroup of HD threads per query head.  The splits'
-// (m, l) go through LDS with one weight c_s = 2^(m_s - M) each, then every
-// thread sums c_s * o_s[d] with its loads issued eight at a time.
+// Merge kernel: one workgroup of HD threads per query head; thread d owns
+// output dim d.  With at most 64 splits everything comes in one round trip:
+// lane s of each wave loads split s's (m_s, l_s), every thread loads its
+// o_s[d] for all splits, all before any use.  Each wave then forms M = max m_s
+// and c_s = 2^(m_s - M) in lane s, L = sum l_s c_s by a DPP reduction (both
+// waves compute the same values), and O = sum_s c_s o_s[d] in split order
+// with c_s read from lane s.  More splits (up to kMaxMergeSplits) take the
+// LDS form: (m, l) through LDS, then the o sums eight loads at a time.
 constexpr int kMaxMergeSplits = 1024;
 
 __global__ __launch_bounds__(128) void attn_merge_kernel(float* __restrict__ out, uint16_t* __restrict__ out16,
                                                          const float* __restrict__ ws, int splits) {
     constexpr int HD = 128;
-    __shared__ float cw[kMaxMergeSplits];
-    __shared__ float red[2];
-    const int h = blockIdx.x, d = threadIdx.x;
-    const float* p = ws + static_cast<int64_t>(h) * splits * (HD + 2);
-    float m = -__builtin_inff();
-    for (int s = d; s < splits; s += HD) m = fmaxf(m, p[s * (HD + 2)]);
-    m = block_reduce<2>(m, OpMax{}, red);
-    __syncthreads();
-    float l = 0.0f;
-    for (int s = d; s < splits; s += HD) {
-        const float ls = p[s * (HD + 2) + 1];
-        const float c = ls == 0.0f ? 0.0f : exp2_hw(p[s * (HD + 2)] - m);  // an empty split weighs 0
-        cw[s] = c;
-        l += ls * c;
-    }
-    l = block_reduce<2>(l, OpAdd{}, red);  // its barrier also publishes cw[]
-    float o = 0.0f;
-    constexpr int kBatch = 8;
-    for (int s0 = 0; s0 < splits; s0 += kBatch) {
-        float v[kBatch];
+    constexpr int kRow = HD + 2;
+    const int h = blockIdx.x, d = threadIdx.x, lane = threadIdx.x & (kWave - 1);
+    const float* p = ws + static_cast<int64_t>(h) * splits * kRow;
+    float r;
+    if (splits <= kWave) {
+        const int sl = lane < splits ? lane : 0;  // clamped: a valid split, dropped below
+        uint32_t ml = static_cast<uint32_t>(sl * kRow);
+        asm volatile("" : "+v"(ml));
+        const float m_l = p[ml];
+        const float l_l = p[ml + 1];
+        float os[kWave];
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int s = s0 + b < splits ? s0 + b : s0;  // clamped: a valid split
-            v[b] = p[s * (HD + 2) + 2 + d];
+        for (int b = 0; b < kWave; ++b) {
+            uint32_t ob = static_cast<uint32_t>((b < splits ? b : 0) * kRow + 2 + d);
+            asm volatile("" : "+v"(ob));
+            os[b] = p[ob];
         }
+        __builtin_amdgcn_sched_barrier(0);
+        const bool on = lane < splits;
+        const float M = wave_reduce(on ? m_l : -__builtin_inff(), OpMax{});
+        const float c_l = (!on || l_l == 0.0f) ? 0.0f : exp2_hw(m_l - M);  // an empty split weighs 0
+        const float L = wave_reduce(on ? l_l * c_l : 0.0f, OpAdd{});
+        float O = 0.0f;
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b)
-            if (s0 + b < splits) o = __builtin_fmaf(cw[s0 + b], v[b], o);
+        for (int b = 0; b < kWave; ++b)
+            if (b < splits) O = __builtin_fmaf(readlane(c_l, b), os[b], O);
+        r = L == 0.0f ? 0.0f : O / L;
+    } else {
+        __shared__ float cw[kMaxMergeSplits];
+        __shared__ float red[2];
+        float m = -__builtin_inff();
+        for (int s = d; s < splits; s += HD) m = fmaxf(m, p[s * kRow]);
+        m = block_reduce<2>(m, OpMax{}, red);
+        __syncthreads();
+        float l = 0.0f;
+        for (int s = d; s < splits; s += HD) {
+            const float ls = p[s * kRow + 1];
+            const float c = ls == 0.0f ? 0.0f : exp2_hw(p[s * kRow] - m);
+            cw[s] = c;
+            l += ls * c;
+        }
+        l = block_reduce<2>(l, OpAdd{}, red);  // its barrier also publishes cw[]
+        float o = 0.0f;
+        constexpr int kBatch = 8;
+        for (int s0 = 0; s0 < splits; s0 += kBatch) {
+            float v[kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) v[b] = p[(s0 + b < splits ? s0 + b : s0) * kRow + 2 + d];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b)
+                if (s0 + b < splits) o = __builtin_fmaf(cw[s0 + b], v[b], o);
+        }
+        r = l == 0.0f ? 0.0f : o / l;
     }
-    const float r = l == 0.0f ? 0.0f : o / l;
     if (out) out[static_cast<int64_t>(h) * HD + d] = r;
     if (out16) out16[static_cast<int64_t>(h) * HD + d] = f32_to_f16_bits(r);
 }
