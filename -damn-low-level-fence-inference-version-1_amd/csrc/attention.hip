@@ -25,7 +25,7 @@
 #define FENCE_ATTN_GT_MAX 2
 #endif
 #ifndef FENCE_ATTN_TARGET_WG
-#define FENCE_ATTN_TARGET_WG 512
+#define FENCE_ATTN_TARGET_WG 1024
 #endif
 
 namespace fence {
@@ -424,8 +424,9 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
 
 // out (fp32) and/or out16 (its binary16 rounding, the f32_to_f16 of
 // src/model/qwen3.cu:308 fused) receive the result.
+// ws holds ws_floats floats (the reference's score_buf: n_q * max_ctx).
 int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void* kcv, const void* vcv, int hd,
-                         int n_q, int n_kv, int seq_len, int max_ctx, float* ws, hipStream_t s) {
+                         int n_q, int n_kv, int seq_len, int max_ctx, float* ws, int64_t ws_floats, hipStream_t s) {
     if ((!out && !out16) || !q || !kcv || !vcv || hd <= 0 || n_q <= 0 || n_kv <= 0 || (n_q % n_kv) != 0)
         return FENCE_ERROR_INVALID_VALUE;
     if (out16 && !aligned(out16, 2)) return FENCE_ERROR_INVALID_VALUE;
@@ -436,7 +437,6 @@ int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void
         return FENCE_ERROR_INVALID_VALUE;
     const float scale = 1.0f / sqrtf(static_cast<float>(hd));
     const float scale2 = scale * 1.44269504088896340736f;  // scores in log2 units for exp2
-    const int64_t ws_floats = static_cast<int64_t>(n_q) * max_ctx;  // the reference's score_buf size
     const int group = n_q / n_kv;
     const bool vec = hd == 128 && aligned(q, 16) && aligned(kc, 16) && aligned(vc, 16);
     if (vec) {
@@ -450,7 +450,8 @@ int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void
         // group 3: masked
         return launch_split<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
     }
-    if (!ws) return FENCE_ERROR_INVALID_VALUE;  // the generic path keeps scores in score_buf
+    // the generic path keeps scores in score_buf, n_q rows of max_ctx
+    if (!ws || ws_floats < static_cast<int64_t>(n_q) * max_ctx) return FENCE_ERROR_INVALID_VALUE;
     return launch(attn_generic_kernel, dim3(static_cast<unsigned>(n_q)), dim3(256), 0, s, out, out16, ws, q, kc, vc,
                   hd, n_q, n_kv, seq_len, max_ctx, scale);
 }
@@ -486,15 +487,17 @@ extern "C" int fence_gqa_attention(float* attn_out, const float* q, const void* 
                                    float* score_buf, hipStream_t stream) {
     if (!attn_out) return FENCE_ERROR_INVALID_VALUE;
     return fence::gqa_attention_launch(attn_out, nullptr, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads,
-                                       seq_len, max_ctx, score_buf, stream);
+                                       seq_len, max_ctx, score_buf, static_cast<int64_t>(n_q_heads) * max_ctx,
+                                       stream);
 }
 
 extern "C" int fence_gqa_attention_f16(float* attn_out, void* out_f16, const float* q, const void* k_cache,
                                        const void* v_cache, int head_dim, int n_q_heads, int n_kv_heads, int seq_len,
-                                       int max_ctx, float* score_buf, hipStream_t stream) {
-    if (!out_f16) return FENCE_ERROR_INVALID_VALUE;
+                                       int max_ctx, float* score_buf, int64_t score_buf_floats, hipStream_t stream) {
+    if (!out_f16 || score_buf_floats < 0) return FENCE_ERROR_INVALID_VALUE;
+    if (score_buf_floats == 0) score_buf_floats = static_cast<int64_t>(n_q_heads) * max_ctx;
     return fence::gqa_attention_launch(attn_out, static_cast<uint16_t*>(out_f16), q, k_cache, v_cache, head_dim,
-                                       n_q_heads, n_kv_heads, seq_len, max_ctx, score_buf, stream);
+                                       n_q_heads, n_kv_heads, seq_len, max_ctx, score_buf, score_buf_floats, stream);
 }
 
 extern "C" int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v, int pos, int kv_dim,

@@ -21,6 +21,9 @@ namespace {
 constexpr size_t kAlign = 256;
 constexpr size_t kStageBytes = size_t(64) << 20;  // one pinned staging buffer
 constexpr int kCopyThreads = 4;                  // host threads filling a staging buffer
+// score_buf holds kScoreBufScale x the reference's n_heads * max_ctx floats:
+// room for four times as many split-sequence partials in decode attention.
+constexpr int kScoreBufScale = 4;
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -309,7 +312,8 @@ bool Qwen3Model::load(const std::string& gguf_path, int max_ctx, hipStream_t str
     // scratch (src/model/qwen3.cu:69-85), one allocation
     const size_t E = c.embed_dim, Q = c.q_dim(), KV = c.kv_dim(), FF = c.ff_dim;
     const size_t half_n = std::max(E, std::max(FF, Q));
-    const size_t f32_sizes[] = {E, E, E, Q, KV, KV, Q, FF, FF, E, size_t(c.vocab_size), size_t(c.n_heads) * max_ctx};
+    const size_t f32_sizes[] = {E, E, E, Q, KV, KV, Q, FF, FF, E, size_t(c.vocab_size),
+                                size_t(kScoreBufScale) * c.n_heads * max_ctx};
     size_t total = 0;
     for (size_t n : f32_sizes) total += align_up(n * 4, kAlign);
     total += align_up(half_n * 2, kAlign) + align_up(FF * 2, kAlign) + kAlign;
@@ -335,7 +339,7 @@ bool Qwen3Model::load(const std::string& gguf_path, int max_ctx, hipStream_t str
     s.up = reinterpret_cast<float*>(take(FF * 4));
     s.down = reinterpret_cast<float*>(take(E * 4));
     s.logits = reinterpret_cast<float*>(take(size_t(c.vocab_size) * 4));
-    s.score_buf = reinterpret_cast<float*>(take(size_t(c.n_heads) * max_ctx * 4));
+    s.score_buf = reinterpret_cast<float*>(take(size_t(kScoreBufScale) * c.n_heads * max_ctx * 4));
     s.x_half = reinterpret_cast<__half*>(take(half_n * 2));
     s.act_half = reinterpret_cast<__half*>(take(FF * 2));
     s.argmax_out = reinterpret_cast<int*>(take(sizeof(int)));
@@ -448,7 +452,8 @@ bool Qwen3Model::forward_fused(int token_id, int pos) {
                                                c.max_ctx, 1, c.n_heads, c.n_kv_heads, c.head_dim, c.rms_eps, nullptr,
                                                pos, c.rope_freq_base, FENCE_ROPE_NEOX, st));
         FENCE_STEP(fence_gqa_attention_f16(nullptr, s.x_half, s.q, kv_cache.k[l], kv_cache.v[l], c.head_dim,
-                                           c.n_heads, c.n_kv_heads, pos + 1, c.max_ctx, s.score_buf, st));
+                                           c.n_heads, c.n_kv_heads, pos + 1, c.max_ctx, s.score_buf,
+                                           kScoreBufScale * int64_t(c.n_heads) * c.max_ctx, st));
         FENCE_STEP(fence_gemv_q6k(w.attn_output, s.x_half, s.down, E, c.q_dim(), st));
         FENCE_STEP(fence_residual_rms_norm_f16(s.hidden, s.down, w.ffn_norm, nullptr, s.x_half, 1, E, c.rms_eps, st));
         FENCE_STEP(fence_gemv_q6k_swiglu_f16(w.ffn_gate, w.ffn_up, s.x_half, s.act_half, nullptr, c.ff_dim, E, st));

@@ -53,7 +53,7 @@ SIGNATURES = {
     "fence_rms_norm_rows": (_P, _P, _P, _L, _I, _F, _P),
     "fence_rope": (_P, _P, _L, _I, _I, _I, _P, _I, _F, _I, _P),
     "fence_qk_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
-    "fence_gqa_attention_f16": (_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P),
+    "fence_gqa_attention_f16": (_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _L, _P),
     "fence_qk_norm_rope_store_kv": (_P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_rms_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_swiglu": (_P, _P, _P, _L, _P),
@@ -223,9 +223,9 @@ def qk_norm_rope(q, k, q_norm_w, k_norm_w, tokens, n_q_heads, n_kv_heads, head_d
 
 
 def gqa_attention_f16(attn_out, out_f16, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, seq_len, max_ctx,
-                      score_buf, stream=None):
+                      score_buf, score_buf_floats=0, stream=None):
     _call("fence_gqa_attention_f16", attn_out, out_f16, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads,
-          seq_len, max_ctx, score_buf, stream)
+          seq_len, max_ctx, score_buf, score_buf_floats, stream)
 
 
 def qk_norm_rope_store_kv(q, k, v, wq, wk, k_cache, v_cache, max_ctx, tokens, n_q_heads, n_kv_heads, head_dim,

@@ -196,11 +196,16 @@ int fence_qk_norm_rope(float* q, float* k, const float* q_norm_w,
 /* fence_gqa_attention with its conversion for the o projection
  * (src/model/qwen3.cu:304-308: gqa_attention, then f32_to_f16 of attn_out)
  * in the same launches: out_f16 [n_q_heads][head_dim] = binary16 of the
- * result, bit-identical to the two calls; attn_out (fp32) may be NULL. */
+ * result; attn_out (fp32) may be NULL.  score_buf_floats is score_buf's size
+ * in floats (0: the reference's n_q_heads * max_ctx).  A larger buffer lets
+ * the sequence be split over more workgroups (partials of n_q_heads * 130
+ * floats per split); with the reference's size the result is bit-identical to
+ * fence_gqa_attention + fence_f32_to_f16. */
 int fence_gqa_attention_f16(float* attn_out, void* out_f16, const float* q,
                             const void* k_cache, const void* v_cache, int head_dim,
                             int n_q_heads, int n_kv_heads, int seq_len, int max_ctx,
-                            float* score_buf, hipStream_t stream);
+                            float* score_buf, int64_t score_buf_floats,
+                            hipStream_t stream);
 
 /* fence_qk_norm_rope, then store_kv of the rotated k and of v, in one pass
  * (src/model/qwen3.cu:293-300): after the norm and RoPE of token t's q and k

@@ -95,7 +95,7 @@ struct ScratchBuffers {
     float* up = nullptr;         // [ff_dim]
     float* down = nullptr;       // [embed_dim]
     float* logits = nullptr;     // [vocab_size]
-    float* score_buf = nullptr;  // [n_heads * max_ctx]
+    float* score_buf = nullptr;  // [4 * n_heads * max_ctx]: attention's split-sequence partials
     __half* x_half = nullptr;    // [max(embed_dim, ff_dim, q_dim)]
     int* argmax_out = nullptr;   // [1]
     __half* act_half = nullptr;  // [ff_dim]: SwiGLU output of the fused sequence

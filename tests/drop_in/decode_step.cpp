@@ -157,7 +157,7 @@ struct Scratch {  // the reference's ScratchBuffers (src/model/qwen3.h:91-112)
         hidden = dalloc<float>(E), residual = dalloc<float>(E), normed = dalloc<float>(E), q = dalloc<float>(QD),
         k = dalloc<float>(KVD), v = dalloc<float>(KVD), attn_out = dalloc<float>(QD), gate = dalloc<float>(FF),
         up = dalloc<float>(FF), tmp = dalloc<float>(E), logits = dalloc<float>(V),
-        score_buf = dalloc<float>(static_cast<size_t>(NQ) * CTX);
+        score_buf = dalloc<float>(4 * static_cast<size_t>(NQ) * CTX);  // 4x: more attention splits
         x_half = dalloc<half>(FF);
         act_half = dalloc<half>(FF);
         argmax_out = dalloc<int>(1);
@@ -205,7 +205,8 @@ void layer_fused(const Layer& L, Scratch& s, int pos, hipStream_t st) {
     fence_gemv_q6k_multi(3, w_qkv, y_qkv, nullptr, m_qkv, s.x_half, E, st);
     fence_qk_norm_rope_store_kv(s.q, s.k, s.v, L.q_norm, L.k_norm, L.kc, L.vc, CTX, 1, NQ, NKV, HD, EPS, nullptr, pos,
                                 BASE, FENCE_ROPE_NEOX, st);
-    fence_gqa_attention_f16(nullptr, s.x_half, s.q, L.kc, L.vc, HD, NQ, NKV, pos + 1, CTX, s.score_buf, st);
+    fence_gqa_attention_f16(nullptr, s.x_half, s.q, L.kc, L.vc, HD, NQ, NKV, pos + 1, CTX, s.score_buf,
+                            4 * int64_t(NQ) * CTX, st);
     fence_gemv_q6k(L.wo, s.x_half, s.tmp, E, QD, st);
     fence_residual_rms_norm_f16(s.hidden, s.tmp, L.ffn_norm, nullptr, s.x_half, 1, E, EPS, st);
     fence_gemv_q6k_swiglu_f16(L.wg, L.wu, s.x_half, s.act_half, nullptr, FF, E, st);

@@ -99,8 +99,10 @@ def _raw(name):
     ("fence_gemv_q6k", (0x1001, 32, 48, 8, 256, None)),           # W not 2-byte aligned
     ("fence_gemv_q6k", (16, 32, 48, 8, 0, None)),                 # K == 0
     ("fence_gemv_q6k_bias", (16, 32, None, 48, 8, 256, None)),    # bias missing
-    ("fence_gqa_attention_f16", (16, None, 32, 48, 64, 128, 8, 2, 10, 100, 80, None)),  # out_f16 missing
-    ("fence_gqa_attention_f16", (None, 0x1001, 32, 48, 64, 128, 8, 2, 10, 100, 80, None)),  # misaligned
+    ("fence_gqa_attention_f16", (16, None, 32, 48, 64, 128, 8, 2, 10, 100, 80, 0, None)),  # out_f16 missing
+    ("fence_gqa_attention_f16", (None, 0x1001, 32, 48, 64, 128, 8, 2, 10, 100, 80, 0, None)),  # misaligned
+    ("fence_gqa_attention_f16", (None, 96, 32, 48, 64, 128, 8, 2, 10, 100, 80, -1, None)),  # negative size
+    ("fence_gqa_attention_f16", (None, 96, 32, 48, 64, 96, 8, 2, 10, 100, 80, 100, None)),  # generic: too small
     ("fence_qk_norm_rope_store_kv", (16, 32, 48, 64, 80, None, 96, 100, 1, 4, 2, 128, 1e-6, None, 0, 1e6, 0,
                                      None)),                        # k_cache missing
     ("fence_qk_norm_rope_store_kv", (16, 32, 48, 64, None, 96, 112, 100, 1, 4, 2, 128, 1e-6, None, 0, 1e6, 0,

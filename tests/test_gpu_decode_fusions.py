@@ -41,7 +41,7 @@ def test_attention_f16_equals_attention_then_conversion(oracle, hd, n_q, n_kv, s
                     ws.data_ptr(), stream())
     F.f32_to_f16(ref16.data_ptr(), ref32.data_ptr(), n_q * hd, stream())
     F.gqa_attention_f16(got32.data_ptr() if with_fp32 else None, got16.data_ptr(), qd.data_ptr(), kd.data_ptr(),
-                        vd.data_ptr(), hd, n_q, n_kv, seq, ctx, ws.data_ptr(), stream())
+                        vd.data_ptr(), hd, n_q, n_kv, seq, ctx, ws.data_ptr(), stream=stream())
     assert np.array_equal(host(got16), host(ref16))
     if with_fp32:
         assert np.array_equal(host(got32).view(np.uint32), host(ref32).view(np.uint32))
@@ -49,6 +49,33 @@ def test_attention_f16_equals_attention_then_conversion(oracle, hd, n_q, n_kv, s
         r = oracle.f32_to_f16(oracle.gqa_attention(q, kc, vc, n_q, n_kv, hd, seq))
         diff = np.abs(host(got16).view(np.float16).astype(np.float64) - r.view(np.float16).astype(np.float64))
         assert np.max(diff) <= 2.0 ** -10 * np.max(np.abs(r.view(np.float16).astype(np.float64)))
+
+
+@pytest.mark.parametrize("seq", [1, 65, 700, 2916, 4096])
+def test_attention_f16_larger_workspace(oracle, seq):
+    """score_buf four times the reference's size: more splits, the same
+    result within the attention bar (and exactly V[0] at one position)."""
+    torch = torch_mod()
+    n_q, n_kv, hd, ctx = 32, 8, 128, 4096
+    rng = np.random.default_rng(seq + 5)
+    kc, vc = caches(rng, ctx, n_kv * hd)
+    q = (rng.standard_normal(n_q * hd) * 0.3).astype(np.float32)
+    ws = torch.empty(4 * n_q * ctx, dtype=torch.float32, device="cuda")
+    got32 = torch.full((n_q * hd,), float("nan"), dtype=torch.float32, device="cuda")
+    got16 = torch.empty(n_q * hd, dtype=torch.int16, device="cuda")
+    LIVE.extend([ws, got32, got16])
+    F.gqa_attention_f16(got32.data_ptr(), got16.data_ptr(), dev(q).data_ptr(), dev(kc.view(np.int16)).data_ptr(),
+                        dev(vc.view(np.int16)).data_ptr(), hd, n_q, n_kv, seq, ctx, ws.data_ptr(), 4 * n_q * ctx,
+                        stream())
+    got = host(got32).reshape(n_q, hd).astype(np.float64)
+    ref = oracle.gqa_attention(q, kc, vc, n_q, n_kv, hd, seq).reshape(n_q, hd)
+    V = np.abs(vc[:seq].view(np.float16).astype(np.float64).reshape(-1, n_kv, hd))
+    for h in range(n_q):
+        assert np.max(np.abs(got[h] - ref[h])) <= 1e-5 * V[:, h // 4, :].max(), f"head {h}"
+    assert np.array_equal(host(got16).view(np.uint16), host(got32).astype(np.float16).view(np.uint16))
+    if seq == 1:
+        v0 = vc[0].view(np.float16).astype(np.float32).reshape(n_kv, hd)
+        assert np.array_equal(host(got32).reshape(n_q, hd), v0[np.arange(n_q) // 4])
 
 
 def run_fused_kv(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, pos0, base, style, offset=0):
