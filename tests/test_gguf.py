@@ -8,6 +8,7 @@ tensor data (sparse, so the >3 GB file costs no disk).  The other tests pin
 the format rules the reference's parser implements and the malformed-file
 checks this reader adds.
 """
+import ctypes
 import struct
 
 import numpy as np
@@ -268,3 +269,48 @@ def test_rejects_deeply_nested_arrays(tmp_path):
     write_gguf(p, [("deep", ARRAY, value), ("k", UINT32, 5)], [])
     with M.GGUF(p) as g:
         assert g.get_u32("k") == 5
+
+
+def test_random_corruptions_never_read_out_of_bounds(tmp_path):
+    """Flip, overwrite or cut random bytes of a valid file's header 400 times:
+    every open either succeeds (and every tensor's data lies inside the file)
+    or fails cleanly with BAD_FILE -- never a crash or an out-of-file read."""
+    rng = np.random.default_rng(2024)
+    p = tmp_path / "ok.gguf"
+    meta = [("general.architecture", STRING, "qwen3"), ("qwen3.block_count", UINT32, 2),
+            ("tok", ARRAY, (STRING, ["a", "bc", "def"])), ("f", FLOAT32, 0.5), ("n", ARRAY, (INT32, [1, 2, 3]))]
+    tensors = [("a", [64], F32, np.arange(64, dtype=np.float32).tobytes()),
+               ("b", [256, 2], Q6_K, bytes(2 * 210)), ("c", [32, 3], Q8_0, bytes(3 * 34))]
+    write_gguf(p, meta, tensors)
+    good = bytearray(p.read_bytes())
+    with M.GGUF(p) as g:
+        header = g.data_offset
+    bad = tmp_path / "bad.gguf"
+    opened = 0
+    for trial in range(400):
+        b = bytearray(good)
+        kind = trial % 3
+        if kind == 0:  # flip bits in a few header bytes
+            for i in rng.integers(0, header, size=int(rng.integers(1, 4))):
+                b[i] ^= int(rng.integers(1, 256))
+        elif kind == 1:  # overwrite a little-endian u64 with something large
+            i = int(rng.integers(0, header - 8))
+            big = [2**63, 2**40, 2**32 - 1, 1 << 20, 2**64 - 1][int(rng.integers(0, 5))]
+            b[i:i + 8] = big.to_bytes(8, "little")
+        else:  # truncate
+            b = b[:int(rng.integers(1, len(b)))]
+        bad.write_bytes(bytes(b))
+        try:
+            g = M.GGUF(bad)
+        except FenceError as e:
+            assert e.status == M.BAD_FILE
+            continue
+        with g:
+            opened += 1
+            for i in range(g.tensor_count):
+                t = g.tensor_at(i)
+                assert g.data_offset + t["offset"] + t["data_size_bytes"] <= g.file_size
+                assert t["n_dims"] <= 4
+                if t["data_size_bytes"]:  # the data is readable: touch its last byte
+                    ctypes.string_at(t["data"] + t["data_size_bytes"] - 1, 1)
+    assert opened > 0  # some mutations land in string bytes and keep the file valid
