@@ -34,10 +34,6 @@
 
 #include "common.hpp"
 
-// 1: a wave issues the next row segment's loads before computing the current one.
-#ifndef FENCE_GEMV_Q6K_PREFETCH
-#define FENCE_GEMV_Q6K_PREFETCH 0
-#endif
 // How a row's blocks are split over waves (see q6_plan): 0 up to four passes
 // (16 blocks) per wave, 1 up to two, 2 one pass where the row allows.
 #ifndef FENCE_GEMV_Q6K_SPLIT
@@ -176,7 +172,7 @@ constexpr int staged_waves() { return PAIR && WPR == 4 ? 8 : 4; }
 // <= 16 blocks.  LDS: one buffer of kSegBytes per wave + red[].  A workgroup
 // of NW waves takes NW / WPR rows per group; with PAIR the first half of them
 // are gate rows and the second half the same rows of up.
-template <int PASSES, int WPR, bool PF, bool PAIR, bool MULTI>
+template <int PASSES, int WPR, bool PAIR, bool MULTI>
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb) {
     constexpr int NW = staged_waves<WPR, PAIR>();
@@ -248,16 +244,6 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
         }
     };
     u4 ch[kChunkSlots];
-    int64_t a0n;
-    int nchn;
-    uint32_t deltan;
-    if constexpr (PF) {
-        int64_t o, lr;
-        int m;
-        row_of(blockIdx.x, &o, &m, &lr);
-        seg_of(lr, &a0n, &nchn, &deltan);
-        load_seg(job.W[m], a0n, nchn, ch);
-    }
     for (int64_t g = blockIdx.x; g * kOutPerGroup < n_out; g += gridDim.x) {
         int64_t o, lr;
         int m;
@@ -267,12 +253,8 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
         int64_t a0;
         int nch;
         uint32_t delta;
-        if constexpr (PF) {
-            a0 = a0n, nch = nchn, delta = deltan;
-        } else {
-            seg_of(lr, &a0, &nch, &delta);
-            load_seg(job.W[m], a0, nch, ch);
-        }
+        seg_of(lr, &a0, &nch, &delta);
+        load_seg(job.W[m], a0, nch, ch);
         if (valid) {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -283,15 +265,6 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
                 const uint32_t dst = cc < nch ? 16u * cc : static_cast<uint32_t>(kBufBytes - 16);
                 *reinterpret_cast<u4*>(buf + dst) = ch[k];
             }
-        }
-        if constexpr (PF) {
-            // the next group's loads fly while this one is computed from LDS
-            int64_t on_, lrn;
-            int mn;
-            row_of(g + gridDim.x, &on_, &mn, &lrn);
-            seg_of(lrn, &a0n, &nchn, &deltan);
-            load_seg(job.W[mn], a0n, nchn, ch);
-            __builtin_amdgcn_sched_barrier(0);
         }
         if (valid) {
             // The lane's block starts at `base` in the buffer for pass 0 and
@@ -451,7 +424,7 @@ int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, hi
     static std::atomic<int> cache[64];
     constexpr int nw = staged_waves<WPR, PAIR>();
     constexpr int out_per_group = PAIR ? nw / WPR / 2 : nw / WPR;
-    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, FENCE_GEMV_Q6K_PREFETCH != 0, PAIR, MULTI>, kWave * nw,
+    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI>, kWave * nw,
                        cache, (n_out + out_per_group - 1) / out_per_group, job, x, nb, s);
 }
 
