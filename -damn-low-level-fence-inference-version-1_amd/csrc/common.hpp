@@ -68,8 +68,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
+// Pairwise (a0^2 + a1^2) + (a2^2 + a3^2), four products and three sums with
+// no fused multiply-add: the same rounding wherever it is inlined, so kernels
+// that sum a row's squares in the same order agree bit for bit.
 __device__ __forceinline__ float dot4(f4 a) {
-    // pairwise: (a0^2 + a1^2) + (a2^2 + a3^2)
+#pragma clang fp contract(off)
     return (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
 }
 
@@ -256,6 +259,22 @@ __device__ __forceinline__ float row_reduce(float v, Op op, float* scratch) {
         return r;
     }
 }
+
+// The vector row RMSNorm's launch shape (rms_norm.hip): threads per row and
+// float4s per lane for rows of n floats.  Its sum of squares is ordered by
+// this shape, so a kernel that normalises a row itself (the Q6_K GEMV's
+// prologue) takes the shape from here to sum in the same order.
+#ifndef FENCE_RMS_VPT
+#define FENCE_RMS_VPT 2
+#endif
+inline bool rms_row_plan(int64_t rows, int n, unsigned* threads, int* vpt) {
+    return plan_row(rows, n / 4, FENCE_RMS_VPT, 8, threads, vpt);
+}
+
+// One row: x16 = binary16(rms_norm(hid + res) * w), hid_out = hid + res (res
+// may be null: the row is hid and hid_out is not written).  rms_norm.hip.
+int residual_rms_f16_launch(float* hid_out, uint16_t* x16, const float* hid, const float* res, const float* w,
+                            int n, float eps, hipStream_t s);
 
 inline unsigned grid_1d(int64_t units, int64_t per_block, int64_t cap = 1 << 30) {
     int64_t g = (units + per_block - 1) / per_block;

@@ -31,6 +31,7 @@
 // 16 blocks are split over 2 or 4 waves of the workgroup, whose partial sums
 // meet in LDS.  The lane's x values (16 per pass) stay in VGPRs for all rows.
 #include <atomic>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -154,6 +155,26 @@ struct Q6Job {
     float* act32;
 };
 
+// NORM launches: x is the layer-boundary row (src/model/qwen3.cu:267-275 and
+// :310-325), h = hid + res (hid alone when res is null) and
+// x = binary16(rms_norm(h) * w), which every workgroup computes in its
+// prologue.  The sum of squares follows the row RMSNorm kernel (rms_norm.hip)
+// at its launch shape for the row, T threads and vpt (1 or 2) float4s per
+// lane: lane f's partial is dot4(float4 f) + dot4(float4 f + T), each 64
+// consecutive lanes reduce as one wave, and the T / 64 wave sums are added
+// in order -- so x is bit-identical to that kernel's.  Workgroup 0 also
+// writes h to hid_out (with res) and x to x_out.
+struct RmsIn {
+    const float* hid;
+    const float* res;
+    float* hid_out;
+    const float* w;
+    uint16_t* x_out;
+    float eps;
+    int T;
+    int vpt;
+};
+
 // Matrix of global row r (wave-uniform), and r's row within it.
 __device__ __forceinline__ int mat_of(const Q6Job& job, int64_t r, int64_t* lr) {
     int m = 0;
@@ -171,10 +192,12 @@ constexpr int staged_waves() { return PAIR && WPR == 4 ? 8 : 4; }
 // Staged kernel.  WPR waves per row (1, 2 or 4), each over at most 4 * PASSES
 // <= 16 blocks.  LDS: one buffer of kSegBytes per wave + red[].  A workgroup
 // of NW waves takes NW / WPR rows per group; with PAIR the first half of them
-// are gate rows and the second half the same rows of up.
-template <int PASSES, int WPR, bool PAIR, bool MULTI>
+// are gate rows and the second half the same rows of up.  NORM: x from
+// `rin` (see RmsIn), staged through the same LDS before the first group's
+// blocks are; NORM (1 or 2) is the norm kernel's float4s per lane, rin.vpt.
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM>
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_staged_kernel(
-    const Q6Job job, const uint16_t* __restrict__ x16, int nb) {
+    const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
     constexpr int NW = staged_waves<WPR, PAIR>();
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
@@ -183,8 +206,13 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
     constexpr int kOutPerGroup = PAIR ? kRowsPerGroup / 2 : kRowsPerGroup;
     static_assert(!PAIR || kRowsPerGroup >= 2, "a pair needs two rows per group");
     constexpr uint32_t kPassBytes = 4 * kBlockBytes;  // 840: a multiple of 4
-    __shared__ __align__(16) uint8_t lds[NW * kBufBytes];
+    // NORM: binary16 x of the longest row this shape takes (nb <= 4 * PASSES * WPR)
+    constexpr int kStageBytes = NW * kBufBytes;
+    constexpr int kNormXBytes = 2 * 1024 * PASSES * WPR;
+    constexpr int kLdsBytes = NORM && kNormXBytes > kStageBytes ? kNormXBytes : kStageBytes;
+    __shared__ __align__(16) uint8_t lds[kLdsBytes];
     __shared__ float red[NW];
+    __shared__ float nred[NORM ? 16 : 1];  // the row norm's wave sums (T <= 1024)
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));  // wave-uniform
     const int seg = wid % WPR;
@@ -198,7 +226,36 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
 
     uint32_t xh[PASSES][8];
     float kb[PASSES][4];
-    load_x<PASSES>(xh, kb, x16, b0, b1, bslot, h, j);
+    if constexpr (!NORM) load_x<PASSES>(xh, kb, x16, b0, b1, bslot, h, j);
+
+    // NORM, first half: the row's loads, issued before the first group's
+    // blocks.  Wave w holds the row norm's waves w, w + NW, ... (vw < T / 64);
+    // a slot past the row holds zeros, as in the norm kernel.
+    // Every load is unconditional (clamped slots, and hidden again in place of
+    // an absent residual), so all are in flight together and none waits for
+    // the blocks issued after them.
+    constexpr int kVW = NORM ? (16 + NW - 1) / NW : 1;
+    constexpr int kVpt = NORM ? NORM : 1;
+    f4 nh[kVW][kVpt], nr[kVW][kVpt], nw[kVW][kVpt];
+    auto norm_slot = [&](int i, int jj, int* f) {
+        const int vw = wid + NW * i;
+        *f = vw * kWave + lane + jj * rin.T;
+        return vw * kWave < rin.T && *f < nb * 64;
+    };
+    if constexpr (NORM != 0) {
+        const float* rp = rin.res ? rin.res : rin.hid;
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) {
+                int f;
+                const int fc = norm_slot(i, jj, &f) ? f : 0;
+                nh[i][jj] = ld4<false>(rin.hid + 4 * fc);
+                nr[i][jj] = ld4<false>(rp + 4 * fc);
+                nw[i][jj] = ld4<false>(rin.w + 4 * fc);
+            }
+        }
+    }
     bool on[PASSES];
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) on[p] = b0 + 4 * p + bslot < b1;
@@ -244,7 +301,73 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
         }
     };
     u4 ch[kChunkSlots];
-    for (int64_t g = blockIdx.x; g * kOutPerGroup < n_out; g += gridDim.x) {
+    if constexpr (NORM != 0) {
+        // Second half, while the first group's blocks are in flight (the loop
+        // below does not load them again): the norm kernel's reduction, x into
+        // LDS, then each lane's x values.
+        {
+            int64_t o, lr, a0;
+            int m, nch;
+            uint32_t delta;
+            row_of(blockIdx.x, &o, &m, &lr);
+            seg_of(lr, &a0, &nch, &delta);
+            load_seg(job.W[m], a0, nch, ch);
+        }
+        // h = hid (+ res), zero past the row; workgroup 0 stores it; then
+        // each slot keeps only w * h, the first product of the norm's output
+        const int nvw = rin.T / kWave;
+        const bool has_res = rin.res != nullptr;
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) {
+                int f;
+                const bool ok = norm_slot(i, jj, &f);
+                const f4 hv = has_res ? nh[i][jj] + nr[i][jj] : nh[i][jj];
+                nh[i][jj] = ok ? hv : f4(0.0f);
+                if (blockIdx.x == 0 && has_res && ok) st4<false>(rin.hid_out + 4 * f, hv);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+            const int vw = wid + NW * i;
+            if (vw < nvw) {  // wave-uniform
+                // the norm kernel's partial: its loop over two float4 slots
+                float ss = 0.0f;
+                ss += dot4(nh[i][0]);
+                ss += kVpt > 1 ? dot4(nh[i][kVpt - 1]) : 0.0f;
+                ss = wave_reduce(ss, OpAdd{});
+                if (lane == 0) nred[vw] = ss;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVW; ++i)
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) nw[i][jj] = nw[i][jj] * nh[i][jj];
+        __syncthreads();
+        float tot = nred[0];
+        for (int v = 1; v < nvw; ++v) tot += nred[v];
+        const float rs = rsqrtf(tot / static_cast<float>(nb * 256) + rin.eps);
+        uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) {
+                int f;
+                if (norm_slot(i, jj, &f)) {
+                    const f4 o = nw[i][jj] * rs;  // (w * h) * rs
+                    st_h4<false>(xs + 4 * f, o);
+                    if (blockIdx.x == 0) st_h4<false>(rin.x_out + 4 * f, o);
+                }
+            }
+        }
+        __syncthreads();
+        load_x<PASSES>(xh, kb, xs, b0, b1, bslot, h, j);
+        __syncthreads();  // lds holds staged blocks from here on
+    }
+    // One row group; LOADED: its blocks are already in ch (the NORM
+    // prologue's first group), so the loop itself loads unconditionally.
+    auto run_group = [&](int64_t g, auto loaded) {
         int64_t o, lr;
         int m;
         row_of(g, &o, &m, &lr);
@@ -254,7 +377,7 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
         int nch;
         uint32_t delta;
         seg_of(lr, &a0, &nch, &delta);
-        load_seg(job.W[m], a0, nch, ch);
+        if constexpr (!decltype(loaded)::value) load_seg(job.W[m], a0, nch, ch);
         if (valid) {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -322,7 +445,13 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
             }
             __syncthreads();  // red[] is rewritten by the next group
         }
+    };
+    int64_t g = blockIdx.x;
+    if constexpr (NORM != 0) {
+        run_group(g, std::true_type{});  // g < the group count: the grid is at most that
+        g += gridDim.x;
     }
+    for (; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::false_type{});
 }
 
 // y . row lr of Wm, summed over the wave (lane 0 holds it): the direct
@@ -397,9 +526,9 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_direct_kernel(const Q6Job j
 
 // A resident grid for `kernel` of `threads` per workgroup: CUs x the
 // occupancy per CU (cached per device in `cache`), at most `groups`.
-template <class Kernel>
-int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t groups, const Q6Job& job,
-                const uint16_t* x, int nb, hipStream_t s) {
+template <class Kernel, class... Args>
+int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t groups, hipStream_t s,
+                const Args&... args) {
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e);
     if (dev < 0 || dev >= 64) return FENCE_ERROR_INVALID_VALUE;
@@ -416,57 +545,67 @@ int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t gro
     }
     if (!FENCE_GEMV_Q6K_RESIDENT) g = 0x7fffffff;
     const unsigned grid = static_cast<unsigned>(groups < g ? groups : g);
-    return launch(kernel, dim3(grid), dim3(threads), 0, s, job, x, nb);
+    return launch(kernel, dim3(grid), dim3(threads), 0, s, args...);
 }
 
-template <int PASSES, int WPR, bool PAIR, bool MULTI>
-int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, hipStream_t s) {
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM>
+int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
     static std::atomic<int> cache[64];
     constexpr int nw = staged_waves<WPR, PAIR>();
     constexpr int out_per_group = PAIR ? nw / WPR / 2 : nw / WPR;
-    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI>, kWave * nw,
-                       cache, (n_out + out_per_group - 1) / out_per_group, job, x, nb, s);
+    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM>, kWave * nw, cache,
+                       (n_out + out_per_group - 1) / out_per_group, s, job, x, nb, rin);
 }
 
 // (PASSES, WPR) of a row of nb blocks: WPR waves per row, each over at most
 // 4 * PASSES blocks.  It depends on nb alone, so every matrix of a multi or
 // pair launch sums its rows in the same order as its own launch would.
-template <bool PAIR, bool MULTI>
-int launch_nb(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, hipStream_t s) {
-    if (FENCE_GEMV_Q6K_SPLIT == 2) {
-        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 8) return launch_staged<1, 2, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 16) return launch_staged<1, 4, PAIR, MULTI>(job, n_out, x, nb, s);
-    } else if (FENCE_GEMV_Q6K_SPLIT == 1) {
-        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 16) return launch_staged<2, 2, PAIR, MULTI>(job, n_out, x, nb, s);
+// NORM launches take rows of up to 32 blocks.
+template <bool PAIR, bool MULTI, int NORM>
+int launch_nb(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
+    if constexpr (FENCE_GEMV_Q6K_SPLIT == 2) {
+        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 8) return launch_staged<1, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 16) return launch_staged<1, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+    } else if constexpr (FENCE_GEMV_Q6K_SPLIT == 1) {
+        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 16) return launch_staged<2, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
     } else {
-        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 12) return launch_staged<3, 1, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 16) return launch_staged<4, 1, PAIR, MULTI>(job, n_out, x, nb, s);
-        if (nb <= 24) return launch_staged<3, 2, PAIR, MULTI>(job, n_out, x, nb, s);
+        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 12) return launch_staged<3, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 16) return launch_staged<4, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 24) return launch_staged<3, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        if (nb <= 32) return launch_staged<4, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
     }
-    if (FENCE_GEMV_Q6K_SPLIT == 0 && nb <= 32) return launch_staged<4, 2, PAIR, MULTI>(job, n_out, x, nb, s);
-    if (nb <= 32) return launch_staged<2, 4, PAIR, MULTI>(job, n_out, x, nb, s);
-    if (nb <= 48) return launch_staged<3, 4, PAIR, MULTI>(job, n_out, x, nb, s);
-    return launch_staged<4, 4, PAIR, MULTI>(job, n_out, x, nb, s);
+    if (nb <= 32) return launch_staged<2, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+    if constexpr (NORM != 0) {
+        return FENCE_ERROR_INVALID_VALUE;  // not dispatched: the caller checks nb
+    } else {
+        if (nb <= 48) return launch_staged<3, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        return launch_staged<4, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+    }
 }
 
 template <bool PAIR>
 int launch_direct(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, hipStream_t s) {
     static std::atomic<int> cache[64];
-    return launch_grid(gemv_q6k_direct_kernel<PAIR>, kThreads, cache, (n_out + 3) / 4, job, x, nb, s);
+    return launch_grid(gemv_q6k_direct_kernel<PAIR>, kThreads, cache, (n_out + 3) / 4, s, job, x, nb);
 }
 
 // Checks and dispatch of a job whose matrices, rows and outputs are filled in.
-int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s) {
-    if (K <= 0 || (K % 256) != 0 || !xv || !aligned(xv, 2)) return FENCE_ERROR_INVALID_VALUE;
-    const uint16_t* x = static_cast<const uint16_t*>(xv);
+// With `rin` (checked by rms_input) x is computed from it: in the GEMV's own
+// prologue where the row norm would run its vector kernel at a shape the
+// prologue takes, otherwise by that kernel into rin->x_out first.
+int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s, const RmsIn* rin = nullptr) {
+    if (K <= 0 || (K % 256) != 0) return FENCE_ERROR_INVALID_VALUE;
+    if (!rin && (!xv || !aligned(xv, 2))) return FENCE_ERROR_INVALID_VALUE;
     const int nb = K / 256;
     const int64_t n_out = pair ? job.end[0] : job.end[job.n - 1];
-    if (n_out == 0) return FENCE_SUCCESS;
+    if (n_out == 0)  // no rows: the input row is still produced
+        return rin ? residual_rms_f16_launch(rin->hid_out, rin->x_out, rin->hid, rin->res, rin->w, K, rin->eps, s)
+                   : FENCE_SUCCESS;
     bool staged = nb <= 4 * kMaxSegBlocks;
     int prev = 0;
     for (int i = 0; i < job.n; ++i) {
@@ -475,9 +614,60 @@ int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s) {
         if (rows == 0) continue;
         staged = staged && aligned(job.W[i], 16) && (static_cast<int64_t>(rows) * nb) % 8 == 0;
     }
-    if (pair) return staged ? launch_nb<true, false>(job, n_out, x, nb, s) : launch_direct<true>(job, n_out, x, nb, s);
+    const RmsIn none{};
+    if (rin) {
+        RmsIn r = *rin;
+        unsigned T = 0;
+        const bool vec_norm = aligned(r.hid, 16) && aligned(r.w, 16) && aligned(r.x_out, 8) &&
+                              (!r.res || (aligned(r.res, 16) && aligned(r.hid_out, 16)));
+        // Two float4 per lane double the prologue's registers: measured on
+        // MI355X, q/k/v at K = 5120 still gain (18.8 -> 15.2 us against the
+        // two launches) but gate/up, whose workgroups loop over many more row
+        // groups, lose at the lower occupancy (40.8 -> 48.2 us), so a pair
+        // takes the two launches there.
+        if (staged && nb <= 32 && vec_norm && rms_row_plan(1, K, &T, &r.vpt) && T <= 1024 &&
+            (r.vpt == 1 || (r.vpt == 2 && !pair))) {
+            r.T = static_cast<int>(T);
+            if (r.vpt == 1)
+                return pair ? launch_nb<true, false, 1>(job, n_out, nullptr, nb, r, s)
+                            : launch_nb<false, true, 1>(job, n_out, nullptr, nb, r, s);
+            return launch_nb<false, true, 2>(job, n_out, nullptr, nb, r, s);
+        }
+        if (int st = residual_rms_f16_launch(r.hid_out, r.x_out, r.hid, r.res, r.w, K, r.eps, s)) return st;
+        xv = r.x_out;
+    }
+    const uint16_t* x = static_cast<const uint16_t*>(xv);
+    if (pair)
+        return staged ? launch_nb<true, false, 0>(job, n_out, x, nb, none, s) : launch_direct<true>(job, n_out, x, nb, s);
     if (!staged) return launch_direct<false>(job, n_out, x, nb, s);
-    return job.n > 1 ? launch_nb<false, true>(job, n_out, x, nb, s) : launch_nb<false, false>(job, n_out, x, nb, s);
+    return job.n > 1 ? launch_nb<false, true, 0>(job, n_out, x, nb, none, s)
+                     : launch_nb<false, false, 0>(job, n_out, x, nb, none, s);
+}
+
+// Whether byte ranges [a, a + an) and [b, b + bn) share a byte (null: no).
+bool overlap(const void* a, size_t an, const void* b, size_t bn) {
+    if (!a || !b) return false;
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + bn && y < x + an;
+}
+
+// A fence_rms_input for rows of K floats: required pointers, alignment, and
+// no output overlapping an input (workgroup 0 writes them while the others
+// read).
+int rms_input(const fence_rms_input* in, int K, RmsIn* r) {
+    if (!in || !in->hidden || !in->weight || !in->x_f16 || (in->residual && !in->hidden_out))
+        return FENCE_ERROR_INVALID_VALUE;
+    if (!aligned(in->hidden, 4) || !aligned(in->weight, 4) || !aligned(in->x_f16, 2) ||
+        (in->residual && (!aligned(in->residual, 4) || !aligned(in->hidden_out, 4))))
+        return FENCE_ERROR_INVALID_VALUE;
+    const size_t f = static_cast<size_t>(K) * 4, hb = static_cast<size_t>(K) * 2;
+    float* hout = in->residual ? in->hidden_out : nullptr;
+    if (overlap(hout, f, in->hidden, f) || overlap(hout, f, in->residual, f) || overlap(hout, f, in->weight, f) ||
+        overlap(in->x_f16, hb, in->hidden, f) || overlap(in->x_f16, hb, in->residual, f) ||
+        overlap(in->x_f16, hb, in->weight, f) || overlap(in->x_f16, hb, hout, f))
+        return FENCE_ERROR_INVALID_VALUE;
+    *r = RmsIn{in->hidden, in->residual, hout, in->weight, static_cast<uint16_t*>(in->x_f16), in->eps, 0, 0};
+    return FENCE_SUCCESS;
 }
 
 int gemv_q6k_launch(float* y, const void* Wv, const void* xv, const float* bias, int M, int K, hipStream_t s) {
@@ -507,11 +697,13 @@ extern "C" int fence_gemv_q6k_bias(const void* W, const void* x, const float* bi
     return fence::gemv_q6k_launch(y, W, x, bias, M, K, stream);
 }
 
-extern "C" int fence_gemv_q6k_multi(int n, const void* const* W, float* const* y, const float* const* bias,
-                                    const int* M, const void* x, int K, hipStream_t stream) {
-    using namespace fence;
+namespace fence {
+namespace {
+
+// The job of a multi launch: n matrices of M[i] rows.
+int multi_job(int n, const void* const* W, float* const* y, const float* const* bias, const int* M, Q6Job* job) {
     if (n < 1 || n > kMaxMats || !W || !y || !M) return FENCE_ERROR_INVALID_VALUE;
-    Q6Job job{};
+    *job = Q6Job{};
     int64_t total = 0;
     for (int i = 0; i < n; ++i) {
         if (M[i] < 0) return FENCE_ERROR_INVALID_VALUE;
@@ -520,32 +712,73 @@ extern "C" int fence_gemv_q6k_multi(int n, const void* const* W, float* const* y
             return FENCE_ERROR_INVALID_VALUE;
         total += M[i];
         if (total > 0x7fffffff) return FENCE_ERROR_INVALID_VALUE;
-        job.W[i] = static_cast<const uint8_t*>(W[i]);
-        job.y[i] = y[i];
-        job.bias[i] = bias ? bias[i] : nullptr;
-        job.end[i] = static_cast<int>(total);
+        job->W[i] = static_cast<const uint8_t*>(W[i]);
+        job->y[i] = y[i];
+        job->bias[i] = bias ? bias[i] : nullptr;
+        job->end[i] = static_cast<int>(total);
     }
-    job.n = n;
+    job->n = n;
+    return FENCE_SUCCESS;
+}
+
+// The job of a gate/up pair of M rows each.
+int pair_job(const void* W_gate, const void* W_up, void* out_f16, float* out, int M, Q6Job* job) {
+    if (M < 0 || M > 0x3fffffff) return FENCE_ERROR_INVALID_VALUE;
+    if (M > 0 && (!W_gate || !W_up || !out_f16 || !aligned(W_gate, 2) || !aligned(W_up, 2) ||
+                  !aligned(out_f16, 2) || (out && !aligned(out, 4))))
+        return FENCE_ERROR_INVALID_VALUE;
+    *job = Q6Job{};
+    job->W[0] = static_cast<const uint8_t*>(W_gate);
+    job->W[1] = static_cast<const uint8_t*>(W_up);
+    job->end[0] = M;
+    job->end[1] = 2 * M;  // rows of up follow gate's (row counts for the staging checks)
+    job->n = 2;
+    job->act16 = static_cast<uint16_t*>(out_f16);
+    job->act32 = out;
+    return FENCE_SUCCESS;
+}
+
+}  // namespace
+}  // namespace fence
+
+extern "C" int fence_gemv_q6k_multi(int n, const void* const* W, float* const* y, const float* const* bias,
+                                    const int* M, const void* x, int K, hipStream_t stream) {
+    using namespace fence;
+    Q6Job job;
+    if (int st = multi_job(n, W, y, bias, M, &job)) return st;
     if (K < 0 || K % 256 != 0) return FENCE_ERROR_INVALID_VALUE;
-    if (total == 0) return FENCE_SUCCESS;
+    if (job.end[n - 1] == 0) return FENCE_SUCCESS;
     return gemv_q6k_run(job, x, K, false, stream);
 }
 
 extern "C" int fence_gemv_q6k_swiglu_f16(const void* W_gate, const void* W_up, const void* x, void* out_f16,
                                          float* out, int M, int K, hipStream_t stream) {
     using namespace fence;
-    if (M < 0 || M > 0x3fffffff || K < 0 || K % 256 != 0) return FENCE_ERROR_INVALID_VALUE;
+    Q6Job job;
+    if (int st = pair_job(W_gate, W_up, out_f16, out, M, &job)) return st;
+    if (K < 0 || K % 256 != 0) return FENCE_ERROR_INVALID_VALUE;
     if (M == 0) return FENCE_SUCCESS;
-    if (!W_gate || !W_up || !out_f16 || !aligned(W_gate, 2) || !aligned(W_up, 2) || !aligned(out_f16, 2) ||
-        (out && !aligned(out, 4)))
-        return FENCE_ERROR_INVALID_VALUE;
-    Q6Job job{};
-    job.W[0] = static_cast<const uint8_t*>(W_gate);
-    job.W[1] = static_cast<const uint8_t*>(W_up);
-    job.end[0] = M;
-    job.end[1] = 2 * M;  // rows of up follow gate's (row counts for the staging checks)
-    job.n = 2;
-    job.act16 = static_cast<uint16_t*>(out_f16);
-    job.act32 = out;
     return gemv_q6k_run(job, x, K, true, stream);
+}
+
+extern "C" int fence_gemv_q6k_multi_rms(int n, const void* const* W, float* const* y, const float* const* bias,
+                                        const int* M, const fence_rms_input* in, int K, hipStream_t stream) {
+    using namespace fence;
+    Q6Job job;
+    RmsIn r;
+    if (int st = multi_job(n, W, y, bias, M, &job)) return st;
+    if (K <= 0 || K % 256 != 0) return FENCE_ERROR_INVALID_VALUE;
+    if (int st = rms_input(in, K, &r)) return st;
+    return gemv_q6k_run(job, nullptr, K, false, stream, &r);
+}
+
+extern "C" int fence_gemv_q6k_swiglu_rms_f16(const void* W_gate, const void* W_up, const fence_rms_input* in,
+                                             void* out_f16, float* out, int M, int K, hipStream_t stream) {
+    using namespace fence;
+    Q6Job job;
+    RmsIn r;
+    if (int st = pair_job(W_gate, W_up, out_f16, out, M, &job)) return st;
+    if (K <= 0 || K % 256 != 0) return FENCE_ERROR_INVALID_VALUE;
+    if (int st = rms_input(in, K, &r)) return st;
+    return gemv_q6k_run(job, nullptr, K, true, stream, &r);
 }

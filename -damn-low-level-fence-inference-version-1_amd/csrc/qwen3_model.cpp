@@ -15,6 +15,7 @@
 #include <stdexcept>
 #include <thread>
 #include <unordered_map>
+#include <utility>
 
 namespace {
 
@@ -424,28 +425,34 @@ bool Qwen3Model::forward_reference(int token_id, int pos) {
 
 // The same step with the sub-block outputs kept apart from the residual
 // stream: each projection back to embed_dim (o, down) writes `down`, and the
-// next RMSNorm adds it into `hidden` in the same pass (hidden + down is the
-// reference's residual_add(hidden = o, residual), the same sum).  q, k and v
-// are one launch; QK-norm, RoPE and the KV store another; attention writes
-// the binary16 input of the o projection itself; gate, up and SwiGLU are one
-// launch (writing act_half, since x_half is still being read).  9 calls per
-// layer instead of 22 plus two copies; every result is bit-identical to the
-// reference sequence's.
+// next RMSNorm adds it into the stream in the same pass (hidden + down is the
+// reference's residual_add(hidden = o, residual), the same sum).  That norm
+// runs inside the projection that reads it: every workgroup of the q/k/v and
+// the gate/up launches normalises the row itself, and one of them writes the
+// new stream row -- into the other of two buffers (hidden, residual), since the
+// rest still read the old one.  q, k and v are one launch; QK-norm, RoPE and
+// the KV store another; attention writes the binary16 input of the o
+// projection itself; gate, up and SwiGLU are one launch (writing act_half).
+// 7 calls per layer instead of 22 plus two copies; every result is
+// bit-identical to the reference sequence's.
 bool Qwen3Model::forward_fused(int token_id, int pos) {
     const Qwen3Config& c = config;
     ScratchBuffers& s = scratch;
     hipStream_t st = stream_;
     const int E = c.embed_dim;
     FENCE_STEP(fence_embed_q8_0(s.hidden, weights.token_embd, token_id, E, st));
-    const float* pending = nullptr;  // a block output not yet added to hidden
+    float* cur = s.hidden;           // the residual stream
+    float* next = s.residual;        // receives cur + a block output
+    const float* pending = nullptr;  // a block output not yet added to the stream
     for (int l = 0; l < c.n_layers; ++l) {
         const Qwen3LayerWeights& w = weights.layers[l];
-        FENCE_STEP(fence_residual_rms_norm_f16(s.hidden, pending, w.attn_norm, nullptr, s.x_half, 1, E, c.rms_eps, st));
         const void* w_qkv[3] = {w.attn_q, w.attn_k, w.attn_v};
         float* y_qkv[3] = {s.q, s.k, s.v};
         const float* b_qkv[3] = {w.attn_q_bias, w.attn_k_bias, w.attn_v_bias};
         const int m_qkv[3] = {c.q_dim(), c.kv_dim(), c.kv_dim()};
-        FENCE_STEP(fence_gemv_q6k_multi(3, w_qkv, y_qkv, b_qkv, m_qkv, s.x_half, E, st));
+        const fence_rms_input attn_in{cur, pending, pending ? next : nullptr, w.attn_norm, s.x_half, c.rms_eps};
+        FENCE_STEP(fence_gemv_q6k_multi_rms(3, w_qkv, y_qkv, b_qkv, m_qkv, &attn_in, E, st));
+        if (pending) std::swap(cur, next);
         const bool qk_norm = w.attn_q_norm && w.attn_k_norm;
         FENCE_STEP(fence_qk_norm_rope_store_kv(s.q, s.k, s.v, qk_norm ? w.attn_q_norm : nullptr,
                                                qk_norm ? w.attn_k_norm : nullptr, kv_cache.k[l], kv_cache.v[l],
@@ -455,12 +462,13 @@ bool Qwen3Model::forward_fused(int token_id, int pos) {
                                            c.n_heads, c.n_kv_heads, pos + 1, c.max_ctx, s.score_buf,
                                            kScoreBufScale * int64_t(c.n_heads) * c.max_ctx, st));
         FENCE_STEP(fence_gemv_q6k(w.attn_output, s.x_half, s.down, E, c.q_dim(), st));
-        FENCE_STEP(fence_residual_rms_norm_f16(s.hidden, s.down, w.ffn_norm, nullptr, s.x_half, 1, E, c.rms_eps, st));
-        FENCE_STEP(fence_gemv_q6k_swiglu_f16(w.ffn_gate, w.ffn_up, s.x_half, s.act_half, nullptr, c.ff_dim, E, st));
+        const fence_rms_input ffn_in{cur, s.down, next, w.ffn_norm, s.x_half, c.rms_eps};
+        FENCE_STEP(fence_gemv_q6k_swiglu_rms_f16(w.ffn_gate, w.ffn_up, &ffn_in, s.act_half, nullptr, c.ff_dim, E, st));
+        std::swap(cur, next);
         FENCE_STEP(fence_gemv_q6k(w.ffn_down, s.act_half, s.down, E, c.ff_dim, st));
         pending = s.down;
     }
-    FENCE_STEP(fence_residual_rms_norm_f16(s.hidden, pending, weights.output_norm, s.normed, nullptr, 1, E, c.rms_eps, st));
+    FENCE_STEP(fence_residual_rms_norm_f16(cur, pending, weights.output_norm, s.normed, nullptr, 1, E, c.rms_eps, st));
     FENCE_STEP(fence_gemv_q8_0(weights.token_embd, s.normed, s.logits, c.vocab_size, E, st));
     return true;
 }

@@ -20,10 +20,6 @@
 
 #include "common.hpp"
 
-#ifndef FENCE_RMS_VPT
-#define FENCE_RMS_VPT 2
-#endif
-
 namespace fence {
 namespace {
 
@@ -139,7 +135,7 @@ int rms_rows_launch(float* out, uint16_t* out16, float* hid, const float* x, con
                      (!res || (aligned(res, 16) && aligned(hid, 16))) && (!out16 || aligned(out16, 8));
     unsigned threads = 0;
     int vpt = 0;
-    if (vec && plan_row(rows, n / 4, FENCE_RMS_VPT, 8, &threads, &vpt)) {
+    if (vec && rms_row_plan(rows, n, &threads, &vpt)) {
         const auto go = [&](auto res_c, auto o32_c, auto o16_c) {
             return launch_vec<decltype(res_c)::value, decltype(o32_c)::value, decltype(o16_c)::value>(
                 grid, threads, vpt, s, out, out16, hid, x, res, w, rows, n, eps);
@@ -158,6 +154,12 @@ int rms_rows_launch(float* out, uint16_t* out16, float* hid, const float* x, con
 }
 
 }  // namespace
+
+int residual_rms_f16_launch(float* hid_out, uint16_t* x16, const float* hid, const float* res, const float* w,
+                            int n, float eps, hipStream_t s) {
+    if (!x16) return FENCE_ERROR_INVALID_VALUE;
+    return rms_rows_launch(nullptr, x16, hid_out, hid, res, w, 1, n, eps, s);
+}
 
 int rms_norm_rows_launch(float* out, const float* x, const float* w, int64_t rows, int n,
                          float eps, hipStream_t s) {

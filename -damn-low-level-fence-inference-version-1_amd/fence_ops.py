@@ -50,6 +50,8 @@ SIGNATURES = {
     "fence_swiglu_f16": (_P, _P, _P, _P, _L, _P),
     "fence_gemv_q6k_multi": (_I, _P, _P, _P, _P, _P, _I, _P),
     "fence_gemv_q6k_swiglu_f16": (_P, _P, _P, _P, _P, _I, _I, _P),
+    "fence_gemv_q6k_multi_rms": (_I, _P, _P, _P, _P, _P, _I, _P),
+    "fence_gemv_q6k_swiglu_rms_f16": (_P, _P, _P, _P, _P, _I, _I, _P),
     "fence_rms_norm_rows": (_P, _P, _P, _L, _I, _F, _P),
     "fence_rope": (_P, _P, _L, _I, _I, _I, _P, _I, _F, _I, _P),
     "fence_qk_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
@@ -70,6 +72,12 @@ SIGNATURES = {
 _RESTYPES = {"fence_status_string": ctypes.c_char_p, "fence_version": ctypes.c_char_p}
 
 _lib = None
+
+
+class RmsInput(ctypes.Structure):
+    """fence_rms_input: h = hidden + residual, x_f16 = binary16(rms_norm(h))."""
+    _fields_ = [("hidden", _P), ("residual", _P), ("hidden_out", _P), ("weight", _P), ("x_f16", _P),
+                ("eps", _F)]
 
 
 class FenceError(RuntimeError):
@@ -204,6 +212,22 @@ def gemv_q6k_multi(Ws, x, ys, Ms, K, biases=None, stream=None):
 
 def gemv_q6k_swiglu_f16(W_gate, W_up, x, out_f16, out, M, K, stream=None):
     _call("fence_gemv_q6k_swiglu_f16", W_gate, W_up, x, out_f16, out, M, K, stream)
+
+
+def rms_input(hidden, residual, hidden_out, weight, x_f16, eps):
+    return RmsInput(hidden, residual, hidden_out, weight, x_f16, eps)
+
+
+def gemv_q6k_multi_rms(Ws, ys, Ms, rin, K, biases=None, stream=None):
+    """As gemv_q6k_multi, with x computed from rin (a RmsInput)."""
+    n = len(Ws)
+    arr = lambda vals: (ctypes.c_void_p * n)(*vals)  # noqa: E731
+    _call("fence_gemv_q6k_multi_rms", n, arr(Ws), arr(ys), None if biases is None else arr(biases),
+          (ctypes.c_int * n)(*Ms), ctypes.byref(rin), K, stream)
+
+
+def gemv_q6k_swiglu_rms_f16(W_gate, W_up, rin, out_f16, out, M, K, stream=None):
+    _call("fence_gemv_q6k_swiglu_rms_f16", W_gate, W_up, ctypes.byref(rin), out_f16, out, M, K, stream)
 
 
 def rms_norm_rows(out, x, w, rows, n, eps, stream=None):

@@ -33,8 +33,9 @@ typedef struct {
 
 /* Which kernel sequence forward launches. */
 enum {
-    FENCE_SEQUENCE_FUSED = 0,     /* fused epilogues and QK-norm + RoPE; q/k/v in one
-                                     launch, gate/up + SwiGLU in another */
+    FENCE_SEQUENCE_FUSED = 0,     /* q/k/v in one launch that also computes its input
+                                     norm, gate/up + SwiGLU (and its norm) in another;
+                                     QK-norm + RoPE + KV store in one */
     FENCE_SEQUENCE_REFERENCE = 1  /* the launch order of src/model/qwen3.cu:267-341 */
 };
 

@@ -266,9 +266,6 @@ int fence_embed_q8_0_gather_rms_norm(float* out, const void* table,
  * Host-side helpers (no device work).
  * ------------------------------------------------------------------------ */
 
-/* inv_freq[p] = 1.0f / powf(freq_base, (float)(2p) / (float)head_dim) for
- * p < head_dim/2 (src/kernels/ops.cuh:133), computed on the host: the RoPE
- * kernels receive exactly these values. */
 /* The layer-boundary epilogue (src/model/qwen3.cu:310-325: residual_add,
  * rms_norm, f32_to_f16) in one pass, on `rows` rows of n:
  * hidden += residual (skipped if residual is NULL; the sum stays in hidden and
@@ -303,6 +300,38 @@ int fence_gemv_q6k_swiglu_f16(const void* W_gate, const void* W_up, const void* 
                               void* out_f16, float* out, int M, int K,
                               hipStream_t stream);
 
+/* The input row of a projection as the layer boundary makes it
+ * (src/model/qwen3.cu:267-278 and 310-325): h = hidden + residual (hidden
+ * alone when residual is NULL), x = binary16(rms_norm(h, weight, eps)). */
+typedef struct {
+    const float* hidden;   /* [K] */
+    const float* residual; /* [K] or NULL */
+    float* hidden_out;     /* [K]: receives h; required with residual, unused without */
+    const float* weight;   /* [K] */
+    void* x_f16;           /* [K] binary16: receives x */
+    float eps;
+} fence_rms_input;
+
+/* fence_gemv_q6k_multi with x computed from `in`: the same results, bit for
+ * bit, as fence_residual_rms_norm_f16 on a copy of hidden (into hidden_out and
+ * x_f16) followed by fence_gemv_q6k_multi on x_f16 -- and one launch where
+ * the norm's vector kernel would run and K <= 8192: every workgroup of the
+ * GEMV normalises the row in its prologue.  hidden_out and x_f16 must not
+ * overlap hidden, residual or weight (so h cannot be formed in place), nor
+ * each other.  K > 0. */
+int fence_gemv_q6k_multi_rms(int n, const void* const* W, float* const* y,
+                             const float* const* bias, const int* M,
+                             const fence_rms_input* in, int K, hipStream_t stream);
+
+/* fence_gemv_q6k_swiglu_f16 with x computed from `in`, as above (one launch
+ * up to K = 4096; beyond, the norm kernel and then the pair). */
+int fence_gemv_q6k_swiglu_rms_f16(const void* W_gate, const void* W_up,
+                                  const fence_rms_input* in, void* out_f16, float* out,
+                                  int M, int K, hipStream_t stream);
+
+/* inv_freq[p] = 1.0f / powf(freq_base, (float)(2p) / (float)head_dim) for
+ * p < head_dim/2 (src/kernels/ops.cuh:133), computed on the host: the RoPE
+ * kernels receive exactly these values. */
 int fence_rope_inv_freq(float* inv_freq, int head_dim, float freq_base);
 
 /* Kernel timing: the next kernel this host thread launches through this

@@ -85,7 +85,7 @@ struct KVCache {
 /* src/model/qwen3.h:91-112 (cpu_logits is the host sampler's). */
 struct ScratchBuffers {
     float* hidden = nullptr;     // [embed_dim]
-    float* residual = nullptr;   // [embed_dim]
+    float* residual = nullptr;   // [embed_dim]: the reference sequence's copy; the fused one's second stream row
     float* normed = nullptr;     // [embed_dim]
     float* q = nullptr;          // [q_dim]
     float* k = nullptr;          // [kv_dim]
@@ -103,8 +103,8 @@ struct ScratchBuffers {
 
 /* The kernel sequence forward() launches. */
 enum class Qwen3Sequence {
-    Fused,      // fused epilogues, q/k/v, QK-norm + RoPE + KV store, attention + conversion,
-                // gate/up + SwiGLU: 9 calls per layer
+    Fused,      // layer-boundary norms inside the q/k/v and gate/up launches, q/k/v, QK-norm +
+                // RoPE + KV store, attention + conversion, gate/up + SwiGLU: 7 calls per layer
     Reference,  // the reference's launcher order, src/model/qwen3.cu:267-341
 };
 

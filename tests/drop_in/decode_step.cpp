@@ -27,6 +27,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <utility>
 #include <vector>
 
 #define HIP_CHECK(call)                                                                    \
@@ -196,20 +197,26 @@ void layer_reference(const Layer& L, Scratch& s, int pos, hipStream_t st) {
 
 // The same layer through the fused entry points.  On entry s.tmp holds the
 // previous block's output still to be added to s.hidden (zeros before the
-// first layer); on exit s.tmp holds this layer's down projection.
+// first layer); on exit s.tmp holds this layer's down projection.  The
+// layer-boundary norms run inside the q/k/v and gate/up launches, which write
+// hidden + tmp into s.residual (their workgroups still read s.hidden); the two
+// pointers then swap, so s.hidden is always the stream -- and after a whole
+// layer (two swaps) the same buffer again.
 void layer_fused(const Layer& L, Scratch& s, int pos, hipStream_t st) {
-    fence_residual_rms_norm_f16(s.hidden, s.tmp, L.attn_norm, nullptr, s.x_half, 1, E, EPS, st);
     const void* w_qkv[3] = {L.wq, L.wk, L.wv};
     float* y_qkv[3] = {s.q, s.k, s.v};
     const int m_qkv[3] = {QD, KVD, KVD};
-    fence_gemv_q6k_multi(3, w_qkv, y_qkv, nullptr, m_qkv, s.x_half, E, st);
+    const fence_rms_input attn_in{s.hidden, s.tmp, s.residual, L.attn_norm, s.x_half, EPS};
+    fence_gemv_q6k_multi_rms(3, w_qkv, y_qkv, nullptr, m_qkv, &attn_in, E, st);
+    std::swap(s.hidden, s.residual);
     fence_qk_norm_rope_store_kv(s.q, s.k, s.v, L.q_norm, L.k_norm, L.kc, L.vc, CTX, 1, NQ, NKV, HD, EPS, nullptr, pos,
                                 BASE, FENCE_ROPE_NEOX, st);
     fence_gqa_attention_f16(nullptr, s.x_half, s.q, L.kc, L.vc, HD, NQ, NKV, pos + 1, CTX, s.score_buf,
                             4 * int64_t(NQ) * CTX, st);
     fence_gemv_q6k(L.wo, s.x_half, s.tmp, E, QD, st);
-    fence_residual_rms_norm_f16(s.hidden, s.tmp, L.ffn_norm, nullptr, s.x_half, 1, E, EPS, st);
-    fence_gemv_q6k_swiglu_f16(L.wg, L.wu, s.x_half, s.act_half, nullptr, FF, E, st);
+    const fence_rms_input ffn_in{s.hidden, s.tmp, s.residual, L.ffn_norm, s.x_half, EPS};
+    fence_gemv_q6k_swiglu_rms_f16(L.wg, L.wu, &ffn_in, s.act_half, nullptr, FF, E, st);
+    std::swap(s.hidden, s.residual);
     fence_gemv_q6k(L.wd, s.act_half, s.tmp, E, FF, st);
 }
 

@@ -139,6 +139,40 @@ def test_invalid_arguments_rejected_on_host(fence, name, args):
     assert _raw(name)(*args) == EINVAL
 
 
+def test_rms_input_entry_points_reject_on_host(fence):
+    """fence_gemv_q6k_multi_rms / fence_gemv_q6k_swiglu_rms_f16: a missing,
+    misaligned or overlapping operand of the input row is EINVAL before any
+    device work (the addresses are never dereferenced)."""
+    L = fence_ops.lib()
+    K = 512
+    hid, res, hout, w, x16 = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    W = (ctypes.c_void_p * 1)(0x60000)
+    y = (ctypes.c_void_p * 1)(0x70000)
+    M = (ctypes.c_int * 1)(8)
+
+    def multi(rin, k=K):
+        return L.fence_gemv_q6k_multi_rms(1, W, y, None, M, None if rin is None else ctypes.byref(rin), k, None)
+
+    def pair(rin, k=K):
+        return L.fence_gemv_q6k_swiglu_rms_f16(0x60000, 0x68000, None if rin is None else ctypes.byref(rin),
+                                               0x78000, None, 8, k, None)
+
+    R = fence_ops.rms_input
+    for call in (multi, pair):
+        assert call(None) == EINVAL
+        assert call(R(hid, res, hid, w, x16, 1e-6)) == EINVAL          # the sum in place
+        assert call(R(hid, res, res + 8, w, x16, 1e-6)) == EINVAL      # overlaps residual
+        assert call(R(hid, res, None, w, x16, 1e-6)) == EINVAL         # residual without hidden_out
+        assert call(R(hid, res, hout, w, None, 1e-6)) == EINVAL        # no x
+        assert call(R(hid, res, hout, None, x16, 1e-6)) == EINVAL      # no weight
+        assert call(R(None, res, hout, w, x16, 1e-6)) == EINVAL        # no hidden
+        assert call(R(hid, res, hout, w, hid + 100, 1e-6)) == EINVAL   # x inside hidden
+        assert call(R(hid, res, hout, w, x16 + 1, 1e-6)) == EINVAL     # x not 2-byte aligned
+        assert call(R(hid + 2, res, hout, w, x16, 1e-6)) == EINVAL     # hidden not 4-byte aligned
+        assert call(R(hid, res, hout, w, x16, 1e-6), k=0) == EINVAL
+        assert call(R(hid, res, hout, w, x16, 1e-6), k=300) == EINVAL
+
+
 def test_zero_sized_calls_are_no_ops(fence):
     assert _raw("fence_rms_norm_rows")(16, 16, 32, 0, 8, 1e-6, None) == 0
     assert _raw("fence_swiglu")(16, 32, 48, 0, None) == 0
