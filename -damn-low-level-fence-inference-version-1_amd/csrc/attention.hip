@@ -19,6 +19,9 @@
 // (m, l, o) per head to the caller's score_buf -- the reference's scratch
 // argument -- and a second kernel merges the splits.  Nothing is allocated.
 #include "common.hpp"
+#include "head_math.hpp"
+
+#include <cmath>
 
 // Workgroups the split-K grid aims for (splits are also capped by score_buf).
 #ifndef FENCE_ATTN_GT_MAX
@@ -46,6 +49,21 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 // reference's fast-math expf also takes (2^(x log2 e)).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Operands of the q and k preparation a split launch does itself when ROPE
+// is set (fence_gqa_attention_qk_f16): qk_norm_rope_store_kv's work
+// (head_ops.hip) for the token at position pos = seq_len - 1, whose q the
+// kernel then reads unprepared.
+struct QkIn {
+    const float* k;   // [n_kv][128]: the token's k and v, before norm and RoPE
+    const float* v;
+    const float* wq;  // [128]: QK-norm weights, or both null (RoPE only)
+    const float* wk;
+    uint16_t* kc;     // the caches, writable: row pos receives the token's k and v
+    uint16_t* vc;
+    float eps;
+    InvFreq tab;
+};
+
 // Split kernel: grid (n_kv * head_groups, splits); HD = 128.  The workgroup
 // walks its positions in sub-chunks of kSub: (A) every 16-lane group scores
 // its positions for the GT heads into LDS, (B) one wave per head takes the
@@ -53,20 +71,35 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // running sum, (C) every lane accumulates p * v for its 8 dims.  The V rows
 // of a sub-chunk are loaded together with its K rows, before phase A.
 // FINAL: one split, write the output; else write (m, l, o) partials to ws.
-template <int GT, bool FINAL>
+// ROPE (kRopeNeox / kRopeInter): a prologue applies QK-norm and RoPE to the
+// workgroup's GT q heads with the head kernels' arithmetic (head_math.hpp),
+// so q is bit-identical to theirs; the workgroups whose range holds position
+// pos also prepare that position's k and v in LDS and attend to it from
+// there (the cache row is never read), and the first head group's one writes
+// the row to the caches.  The first sub-chunk's K and V loads are issued
+// before the prologue, which runs while they are in flight.
+template <int GT, bool FINAL, int ROPE>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict__ out, uint16_t* __restrict__ out16,
                                                               float* __restrict__ ws,
                                                               const float* __restrict__ q,
                                                               const uint16_t* __restrict__ kc,
                                                               const uint16_t* __restrict__ vc, int n_q, int n_kv,
-                                                              int seq_len, int chunk, float scale2) {
+                                                              int seq_len, int chunk, float scale2, const QkIn qk) {
     constexpr int HD = 128;
+    constexpr int HALF = HD / 2;
+    constexpr int G = HD / 8;              // prologue lanes (units) per head
     constexpr int kPG = kThreads / 16;     // position groups (16 lanes each)
     constexpr int kPPG = FENCE_ATTN_PPG;   // positions per group per sub-chunk
     constexpr int kSub = kPG * kPPG;       // positions per sub-chunk
+    constexpr bool QK = ROPE != kRopeNone;
+    constexpr int kUnits = G * (GT + 1);   // prologue: the GT q heads' units, then the k head's
+    static_assert(!QK || (kThreads >= 3 * kWave && kUnits <= 2 * kWave), "prologue lanes");
     __shared__ float sp[GT][kSub];         // scores, then weights p
     __shared__ float hm[GT], hl[GT], hc[GT];
     __shared__ __align__(16) float xo[kPG][GT][HD];
+    __shared__ __align__(16) float qcs[QK ? HD : 1];            // prologue: cos[HALF] then sin[HALF]
+    __shared__ __align__(16) float qs[QK ? GT : 1][HD];         // prologue: the prepared q heads
+    __shared__ __align__(16) uint16_t kvn[QK ? 2 : 1][HD];      // prologue: position pos's k, v (binary16)
     const int group = n_q / n_kv;
     const int head_groups = (group + GT - 1) / GT;
     const int kvh = blockIdx.x / head_groups;
@@ -80,15 +113,19 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
     const int pg = threadIdx.x >> 4;  // position group
     const int sl = lane & 15;         // dims [8 sl, 8 sl + 8)
     const int64_t kv_dim = static_cast<int64_t>(n_kv) * HD;
+    const int pos = seq_len - 1;
+    const bool has_pos = QK && t_begin <= pos && pos < t_end;  // workgroup-uniform
 
     float qv[GT][8];
+    if constexpr (!QK) {
 #pragma unroll
-    for (int g = 0; g < GT; ++g) {
-        const int h = h0 + (g < ng ? g : 0);  // a missing head repeats head h0 and is not written
-        const f4 a = *reinterpret_cast<const f4*>(q + static_cast<int64_t>(h) * HD + 8 * sl);
-        const f4 b = *reinterpret_cast<const f4*>(q + static_cast<int64_t>(h) * HD + 8 * sl + 4);
-        qv[g][0] = a.x, qv[g][1] = a.y, qv[g][2] = a.z, qv[g][3] = a.w;
-        qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
+        for (int g = 0; g < GT; ++g) {
+            const int h = h0 + (g < ng ? g : 0);  // a missing head repeats head h0 and is not written
+            const f4 a = *reinterpret_cast<const f4*>(q + static_cast<int64_t>(h) * HD + 8 * sl);
+            const f4 b = *reinterpret_cast<const f4*>(q + static_cast<int64_t>(h) * HD + 8 * sl + 4);
+            qv[g][0] = a.x, qv[g][1] = a.y, qv[g][2] = a.z, qv[g][3] = a.w;
+            qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
+        }
     }
     float o[GT][8];
 #pragma unroll
@@ -102,16 +139,32 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
 
     const uint16_t* kbase = kc + static_cast<int64_t>(kvh) * HD + 8 * sl;
     const uint16_t* vbase = vc + static_cast<int64_t>(kvh) * HD + 8 * sl;
-    for (int t0 = t_begin; t0 < t_end; t0 += kSub) {
-        h8 kr[kPPG], vr[kPPG];
-        bool on[kPPG];
+    h8 kr[kPPG], vr[kPPG];
+    bool on[kPPG];
+    // The sub-chunk's K and V rows, all loads first.  Clamped: a valid cached
+    // position; with ROPE never row pos, which this launch is writing.
+    auto load_kv = [&](int t0) {
 #pragma unroll
-        for (int i = 0; i < kPPG; ++i) {  // the sub-chunk's K and V rows, all loads first
+        for (int i = 0; i < kPPG; ++i) {
             const int t = t0 + pg + kPG * i;
             on[i] = t < t_end;
-            const int64_t tc = on[i] ? t : t_begin;  // clamped: a valid cached position
+            int64_t tc = on[i] ? t : t_begin;
+            if constexpr (QK) tc = (on[i] && t != pos) ? t : (t_begin != pos ? t_begin : 0);
             kr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(kbase + tc * kv_dim));
             vr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(vbase + tc * kv_dim));
+        }
+    };
+    auto process = [&](int t0) {
+        if constexpr (QK) {
+            if (has_pos) {  // position pos from the prologue's rows
+#pragma unroll
+                for (int i = 0; i < kPPG; ++i) {
+                    if (t0 + pg + kPG * i == pos) {
+                        kr[i] = *reinterpret_cast<const h8*>(&kvn[0][8 * sl]);
+                        vr[i] = *reinterpret_cast<const h8*>(&kvn[1][8 * sl]);
+                    }
+                }
+            }
         }
         // (A) scores, in log2 units
 #pragma unroll
@@ -172,6 +225,72 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
             }
         }
         __syncthreads();  // sp and hc are rewritten by the next sub-chunk
+    };
+
+    if (t_begin < t_end) load_kv(t_begin);
+    if constexpr (QK) {
+        // Unit u < kUnits: q head g = u / G (u < G * GT), else the k head;
+        // elements [4i, 4i + 4) and [HALF + 4i, HALF + 4i + 4), i = u % G.
+        // Whole waves compute (the DPP rows need every lane); lanes past the
+        // units repeat the k unit and store nothing.  Wave 2 computes the
+        // pair angles' cos and sin meanwhile.
+        const int u = threadIdx.x;
+        const bool unit_wave = wave * kWave < kUnits;  // wave-uniform
+        const bool isk = u >= G * GT;
+        const int i = u % G;
+        const int g = isk ? 0 : u / G;
+        f4 a, b, va, vb;
+        if (unit_wave) {
+            const float* src = isk ? qk.k + static_cast<int64_t>(kvh) * HD
+                                   : q + static_cast<int64_t>(h0 + (g < ng ? g : 0)) * HD;
+            const float* vsrc = qk.v + static_cast<int64_t>(kvh) * HD;
+            a = ld4<false>(src + 4 * i);
+            b = ld4<false>(src + HALF + 4 * i);
+            va = ld4<false>(vsrc + 4 * i);
+            vb = ld4<false>(vsrc + HALF + 4 * i);
+            if (qk.wq) {  // launch-uniform
+                const float* w = isk ? qk.wk : qk.wq;
+                head_norm_unit<G>(a, b, ld4<false>(w + 4 * i), ld4<false>(w + HALF + 4 * i), qk.eps);
+            }
+        } else if (wave == 2) {
+            float sn, cn;
+            sincos_angle(static_cast<float>(pos) * qk.tab.v[lane], &sn, &cn);
+            qcs[lane] = cn;
+            qcs[HALF + lane] = sn;
+        }
+        __syncthreads();  // qcs
+        if (unit_wave) {
+            rope_unit<ROPE, G>(a, b, qcs, i);
+            if (!isk) {
+                *reinterpret_cast<f4*>(&qs[g][4 * i]) = a;
+                *reinterpret_cast<f4*>(&qs[g][HALF + 4 * i]) = b;
+            } else if (u < kUnits && has_pos) {
+                st_h4<false>(&kvn[0][4 * i], a);
+                st_h4<false>(&kvn[0][HALF + 4 * i], b);
+                st_h4<false>(&kvn[1][4 * i], va);
+                st_h4<false>(&kvn[1][HALF + 4 * i], vb);
+                if (blockIdx.x % head_groups == 0) {  // one writer per kv head
+                    const int64_t at = static_cast<int64_t>(pos) * kv_dim + static_cast<int64_t>(kvh) * HD;
+                    st_h4<false>(qk.kc + at + 4 * i, a);
+                    st_h4<false>(qk.kc + at + HALF + 4 * i, b);
+                    st_h4<false>(qk.vc + at + 4 * i, va);
+                    st_h4<false>(qk.vc + at + HALF + 4 * i, vb);
+                }
+            }
+        }
+        __syncthreads();  // qs, kvn
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            const f4 a = *reinterpret_cast<const f4*>(&qs[g][8 * sl]);
+            const f4 b = *reinterpret_cast<const f4*>(&qs[g][8 * sl + 4]);
+            qv[g][0] = a.x, qv[g][1] = a.y, qv[g][2] = a.z, qv[g][3] = a.w;
+            qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
+        }
+    }
+    if (t_begin < t_end) process(t_begin);
+    for (int t0 = t_begin + kSub; t0 < t_end; t0 += kSub) {
+        load_kv(t0);
+        process(t0);
     }
 
     // Sum the position groups' outputs (they share the running maximum).
@@ -392,9 +511,9 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int* __restrict__ result, 
     if (threadIdx.x == 0) *result = bi[0];
 }
 
-template <int GT>
+template <int GT, int ROPE>
 int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc, int n_q, int n_kv,
-                 int seq_len, int64_t ws_floats, float scale, hipStream_t s) {
+                 int seq_len, int64_t ws_floats, float scale, const QkIn& qk, hipStream_t s) {
     constexpr int HD = 128;
     const int group = n_q / n_kv;
     const int head_groups = (group + GT - 1) / GT;
@@ -411,13 +530,26 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
     const int chunk = static_cast<int>((seq_len + splits - 1) / splits);
     const dim3 grid(static_cast<unsigned>(base_wg), static_cast<unsigned>(splits));
     if (splits == 1)
-        return launch(attn_split_kernel<GT, true>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc, n_q, n_kv,
-                      seq_len, chunk, scale);
-    if (int st = launch(attn_split_kernel<GT, false>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc, n_q,
-                        n_kv, seq_len, chunk, scale))
+        return launch(attn_split_kernel<GT, true, ROPE>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc, n_q,
+                      n_kv, seq_len, chunk, scale, qk);
+    if (int st = launch(attn_split_kernel<GT, false, ROPE>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc,
+                        n_q, n_kv, seq_len, chunk, scale, qk))
         return st;
     return launch(attn_merge_kernel, dim3(static_cast<unsigned>(n_q)), dim3(HD), 0, s, out, out16, ws,
                   static_cast<int>(splits));
+}
+
+// The split launch for GT heads per workgroup, with the q/k prologue of
+// style `rope` when qk is set.
+template <int GT>
+int launch_split_qk(float* out, uint16_t* out16, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc,
+                    int n_q, int n_kv, int seq_len, int64_t ws_floats, float scale, const QkIn* qk, int rope,
+                    hipStream_t s) {
+    if (!qk)
+        return launch_split<GT, kRopeNone>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, QkIn{}, s);
+    if (rope == kRopeNeox)
+        return launch_split<GT, kRopeNeox>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, *qk, s);
+    return launch_split<GT, kRopeInter>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, *qk, s);
 }
 
 }  // namespace
@@ -425,8 +557,12 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
 // out (fp32) and/or out16 (its binary16 rounding, the f32_to_f16 of
 // src/model/qwen3.cu:308 fused) receive the result.
 // ws holds ws_floats floats (the reference's score_buf: n_q * max_ctx).
+// qk (with style rope): q is unprepared and the launch applies QK-norm, RoPE
+// and the KV store of position seq_len - 1 itself; only on the vector path
+// (the caller checks vec_attention).
 int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void* kcv, const void* vcv, int hd,
-                         int n_q, int n_kv, int seq_len, int max_ctx, float* ws, int64_t ws_floats, hipStream_t s) {
+                         int n_q, int n_kv, int seq_len, int max_ctx, float* ws, int64_t ws_floats, hipStream_t s,
+                         const QkIn* qk = nullptr, int rope = kRopeNone) {
     if ((!out && !out16) || !q || !kcv || !vcv || hd <= 0 || n_q <= 0 || n_kv <= 0 || (n_q % n_kv) != 0)
         return FENCE_ERROR_INVALID_VALUE;
     if (out16 && !aligned(out16, 2)) return FENCE_ERROR_INVALID_VALUE;
@@ -439,16 +575,20 @@ int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void
     const float scale2 = scale * 1.44269504088896340736f;  // scores in log2 units for exp2
     const int group = n_q / n_kv;
     const bool vec = hd == 128 && aligned(q, 16) && aligned(kc, 16) && aligned(vc, 16);
+    if (qk && !vec) return FENCE_ERROR_INVALID_VALUE;
     if (vec) {
         if (FENCE_ATTN_GT_MAX == 1)
-            return launch_split<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+            return launch_split_qk<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
         if (FENCE_ATTN_GT_MAX == 2 && group >= 2)
-            return launch_split<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
-        if (group >= 4) return launch_split<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
-        if (group == 2) return launch_split<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
-        if (group == 1) return launch_split<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+            return launch_split_qk<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+        if (group >= 4)
+            return launch_split_qk<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+        if (group == 2)
+            return launch_split_qk<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+        if (group == 1)
+            return launch_split_qk<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
         // group 3: masked
-        return launch_split<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, s);
+        return launch_split_qk<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
     }
     // the generic path keeps scores in score_buf, n_q rows of max_ctx
     if (!ws || ws_floats < static_cast<int64_t>(n_q) * max_ctx) return FENCE_ERROR_INVALID_VALUE;
@@ -498,6 +638,42 @@ extern "C" int fence_gqa_attention_f16(float* attn_out, void* out_f16, const flo
     if (score_buf_floats == 0) score_buf_floats = static_cast<int64_t>(n_q_heads) * max_ctx;
     return fence::gqa_attention_launch(attn_out, static_cast<uint16_t*>(out_f16), q, k_cache, v_cache, head_dim,
                                        n_q_heads, n_kv_heads, seq_len, max_ctx, score_buf, score_buf_floats, stream);
+}
+
+extern "C" int fence_gqa_attention_qk_f16(float* attn_out, void* out_f16, float* q, float* k, const float* v,
+                                          const float* q_norm_w, const float* k_norm_w, void* k_cache, void* v_cache,
+                                          int head_dim, int n_q_heads, int n_kv_heads, int pos, int max_ctx, float eps,
+                                          float freq_base, int style, float* score_buf, int64_t score_buf_floats,
+                                          hipStream_t stream) {
+    using namespace fence;
+    if (!out_f16 || !q || !k || !v || !k_cache || !v_cache || score_buf_floats < 0) return FENCE_ERROR_INVALID_VALUE;
+    if (pos < 0 || max_ctx < 1 || pos >= max_ctx || n_q_heads <= 0 || n_kv_heads <= 0) return FENCE_ERROR_INVALID_VALUE;
+    if ((q_norm_w == nullptr) != (k_norm_w == nullptr)) return FENCE_ERROR_INVALID_VALUE;
+    if (style != kRopeNeox && style != kRopeInter) return FENCE_ERROR_INVALID_VALUE;
+    if (score_buf_floats == 0) score_buf_floats = static_cast<int64_t>(n_q_heads) * max_ctx;
+    uint16_t* o16 = static_cast<uint16_t*>(out_f16);
+    const bool fused = head_dim == 128 && n_q_heads % n_kv_heads == 0 && freq_base > 0.0f && std::isfinite(freq_base) &&
+                       aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(k_cache, 16) &&
+                       aligned(v_cache, 16) && (!q_norm_w || (aligned(q_norm_w, 16) && aligned(k_norm_w, 16))) &&
+                       (!attn_out || aligned(attn_out, 4)) && aligned(o16, 2) && (!score_buf || aligned(score_buf, 4));
+    if (!fused) {  // the two calls it stands for
+        if (int st = fence_qk_norm_rope_store_kv(q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, max_ctx, 1, n_q_heads,
+                                                 n_kv_heads, head_dim, eps, nullptr, pos, freq_base, style, stream))
+            return st;
+        return gqa_attention_launch(attn_out, o16, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, pos + 1,
+                                    max_ctx, score_buf, score_buf_floats, stream);
+    }
+    QkIn qk{};
+    qk.k = k;
+    qk.v = v;
+    qk.wq = q_norm_w;
+    qk.wk = k_norm_w;
+    qk.kc = static_cast<uint16_t*>(k_cache);
+    qk.vc = static_cast<uint16_t*>(v_cache);
+    qk.eps = eps;
+    rope_inv_freq_host(qk.tab.v, head_dim, freq_base);
+    return gqa_attention_launch(attn_out, o16, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, pos + 1, max_ctx,
+                                score_buf, score_buf_floats, stream, &qk, style);
 }
 
 extern "C" int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v, int pos, int kv_dim,

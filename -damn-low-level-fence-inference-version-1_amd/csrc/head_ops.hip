@@ -17,8 +17,10 @@
 // freq[] is computed on the host (exactly the reference expression) and
 // passed in the kernel arguments; cos/sin of the token's hd/2 angles are
 // computed once per token into LDS and shared by all heads, while the
-// token's loads are in flight.
+// token's loads are in flight.  The per-head arithmetic is head_math.hpp's,
+// which attention.hip shares.
 #include "common.hpp"
+#include "head_math.hpp"
 
 #include <cmath>
 
@@ -28,14 +30,7 @@
 
 namespace fence {
 
-enum { kRopeNone = -1, kRopeNeox = FENCE_ROPE_NEOX, kRopeInter = FENCE_ROPE_INTERLEAVED };
 enum { kNormNone = 0, kNormRow = 1, kNormHead = 2 };
-
-constexpr int kMaxHalf = 128;  // head_dim <= 256 for RoPE
-
-struct InvFreq {
-    float v[kMaxHalf];
-};
 
 // Operands of a head-structured op.  qo/qi: q output/input
 // [tokens][nq][hd]; k: [tokens][nkv][hd], in place; wq/wk: norm weights.
@@ -61,17 +56,6 @@ struct HeadArgs {
 };
 
 namespace {
-
-// sin and cos of an angle given in radians as an exact float (the angle
-// (float)pos * freq[p], bit-identical to the reference's).  The angle is
-// divided by pi and reduced to [-1, 1] in double -- error ~1e-16 for angles
-// up to 2^24 rad -- and sincospif finishes in single precision with no
-// large-argument reduction path.
-__device__ __forceinline__ void sincos_angle(float a, float* s, float* c) {
-    double t = static_cast<double>(a) * 0.31830988618379067154;  // 1/pi
-    t -= 2.0 * __builtin_rint(t * 0.5);
-    sincospif(static_cast<float>(t), s, c);
-}
 
 // MAXS units per lane (exactly: the dispatcher launches MAXS == slots).
 template <int ROPE, int NORM, int G, int MAXS, bool KV>
@@ -185,7 +169,7 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(const HeadArgs args,
 #pragma unroll
             for (int s = 0; s < MAXS; ++s) {
                 const float tot = group_reduce<G>(dot4(a[s]) + dot4(b[s]), OpAdd());
-                rh[s] = rsqrtf(tot / static_cast<float>(HD) + eps);
+                rh[s] = head_rscale(tot, static_cast<float>(HD), eps);
             }
         }
 
@@ -209,27 +193,7 @@ __global__ __launch_bounds__(1024) void head_ops_vec_kernel(const HeadArgs args,
                 va = (wa[s] * va) * rh[s];
                 vb = (wb[s] * vb) * rh[s];
             }
-            if constexpr (ROPE == kRopeNeox) {
-                const f4 c = *reinterpret_cast<const f4*>(cs + 4 * i);
-                const f4 sn = *reinterpret_cast<const f4*>(cs + HALF + 4 * i);
-                const f4 x0 = va, x1 = vb;
-                va = x0 * c - x1 * sn;
-                vb = x0 * sn + x1 * c;
-            } else if constexpr (ROPE == kRopeInter) {
-                const f2 ca = *reinterpret_cast<const f2*>(cs + 2 * i);
-                const f2 sa = *reinterpret_cast<const f2*>(cs + HALF + 2 * i);
-                const f2 cb = *reinterpret_cast<const f2*>(cs + HALF / 2 + 2 * i);
-                const f2 sb = *reinterpret_cast<const f2*>(cs + HALF + HALF / 2 + 2 * i);
-                const f4 x = va, y = vb;
-                va.x = x.x * ca.x - x.y * sa.x;
-                va.y = x.x * sa.x + x.y * ca.x;
-                va.z = x.z * ca.y - x.w * sa.y;
-                va.w = x.z * sa.y + x.w * ca.y;
-                vb.x = y.x * cb.x - y.y * sb.x;
-                vb.y = y.x * sb.x + y.y * cb.x;
-                vb.z = y.z * cb.y - y.w * sb.y;
-                vb.w = y.z * sb.y + y.w * cb.y;
-            }
+            rope_unit<ROPE, G>(va, vb, cs, i);
             float* dst = isq ? qrow_out + h * HD : krow + (h - nq) * HD;
             st4<true>(dst + 4 * i, va);
             st4<true>(dst + HALF + 4 * i, vb);
@@ -293,7 +257,7 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(const HeadArgs arg
                 wr = isq ? wq : wk;
                 float ss = 0.0f;
                 for (int e = lane; e < hd; e += kWave) ss += src[e] * src[e];
-                r = rsqrtf(wave_reduce(ss, OpAdd()) / static_cast<float>(hd) + eps);
+                r = head_rscale(wave_reduce(ss, OpAdd()), static_cast<float>(hd), eps);
             }
             // KV store of this k head: the row of the token's position
             const bool kv = args.kc && !isq && pos >= 0 && pos < args.max_ctx;
@@ -320,7 +284,8 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(const HeadArgs arg
                     }
                     float sn, cn;
                     sincos_angle(static_cast<float>(pos) * tab.v[p], &sn, &cn);
-                    const float y0 = x0 * cn - x1 * sn, y1 = x0 * sn + x1 * cn;
+                    const f2 y = rope_pair(x0, x1, cn, sn);
+                    const float y0 = y.x, y1 = y.y;
                     dst[i0] = y0;
                     dst[i1] = y1;
                     if (kv) {

@@ -430,11 +430,11 @@ bool Qwen3Model::forward_reference(int token_id, int pos) {
 // runs inside the projection that reads it: every workgroup of the q/k/v and
 // the gate/up launches normalises the row itself, and one of them writes the
 // new stream row -- into the other of two buffers (hidden, residual), since the
-// rest still read the old one.  q, k and v are one launch; QK-norm, RoPE and
-// the KV store another; attention writes the binary16 input of the o
-// projection itself; gate, up and SwiGLU are one launch (writing act_half).
-// 7 calls per layer instead of 22 plus two copies; every result is
-// bit-identical to the reference sequence's.
+// rest still read the old one.  q, k and v are one launch; attention applies
+// QK-norm and RoPE to q itself, prepares and stores the new k and v row, and
+// writes the binary16 input of the o projection; gate, up and SwiGLU are one
+// launch (writing act_half).  6 calls per layer instead of 22 plus two
+// copies; every result is bit-identical to the reference sequence's.
 bool Qwen3Model::forward_fused(int token_id, int pos) {
     const Qwen3Config& c = config;
     ScratchBuffers& s = scratch;
@@ -454,13 +454,11 @@ bool Qwen3Model::forward_fused(int token_id, int pos) {
         FENCE_STEP(fence_gemv_q6k_multi_rms(3, w_qkv, y_qkv, b_qkv, m_qkv, &attn_in, E, st));
         if (pending) std::swap(cur, next);
         const bool qk_norm = w.attn_q_norm && w.attn_k_norm;
-        FENCE_STEP(fence_qk_norm_rope_store_kv(s.q, s.k, s.v, qk_norm ? w.attn_q_norm : nullptr,
-                                               qk_norm ? w.attn_k_norm : nullptr, kv_cache.k[l], kv_cache.v[l],
-                                               c.max_ctx, 1, c.n_heads, c.n_kv_heads, c.head_dim, c.rms_eps, nullptr,
-                                               pos, c.rope_freq_base, FENCE_ROPE_NEOX, st));
-        FENCE_STEP(fence_gqa_attention_f16(nullptr, s.x_half, s.q, kv_cache.k[l], kv_cache.v[l], c.head_dim,
-                                           c.n_heads, c.n_kv_heads, pos + 1, c.max_ctx, s.score_buf,
-                                           kScoreBufScale * int64_t(c.n_heads) * c.max_ctx, st));
+        FENCE_STEP(fence_gqa_attention_qk_f16(nullptr, s.x_half, s.q, s.k, s.v, qk_norm ? w.attn_q_norm : nullptr,
+                                              qk_norm ? w.attn_k_norm : nullptr, kv_cache.k[l], kv_cache.v[l],
+                                              c.head_dim, c.n_heads, c.n_kv_heads, pos, c.max_ctx, c.rms_eps,
+                                              c.rope_freq_base, FENCE_ROPE_NEOX, s.score_buf,
+                                              kScoreBufScale * int64_t(c.n_heads) * c.max_ctx, st));
         FENCE_STEP(fence_gemv_q6k(w.attn_output, s.x_half, s.down, E, c.q_dim(), st));
         const fence_rms_input ffn_in{cur, s.down, next, w.ffn_norm, s.x_half, c.rms_eps};
         FENCE_STEP(fence_gemv_q6k_swiglu_rms_f16(w.ffn_gate, w.ffn_up, &ffn_in, s.act_half, nullptr, c.ff_dim, E, st));

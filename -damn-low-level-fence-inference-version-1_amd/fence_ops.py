@@ -57,6 +57,8 @@ SIGNATURES = {
     "fence_qk_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_gqa_attention_f16": (_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _L, _P),
     "fence_qk_norm_rope_store_kv": (_P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
+    "fence_gqa_attention_qk_f16": (_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _I, _P, _L,
+                                   _P),
     "fence_rms_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_swiglu": (_P, _P, _P, _L, _P),
     "fence_softmax_rows": (_P, _L, _I, _L, _P),
@@ -256,6 +258,12 @@ def qk_norm_rope_store_kv(q, k, v, wq, wk, k_cache, v_cache, max_ctx, tokens, n_
                           eps, positions, pos0, freq_base, style, stream=None):
     _call("fence_qk_norm_rope_store_kv", q, k, v, wq, wk, k_cache, v_cache, max_ctx, tokens, n_q_heads,
           n_kv_heads, head_dim, eps, positions, pos0, freq_base, style, stream)
+
+
+def gqa_attention_qk_f16(attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, head_dim, n_q_heads,
+                         n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf, score_buf_floats=0, stream=None):
+    _call("fence_gqa_attention_qk_f16", attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, head_dim,
+          n_q_heads, n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf, score_buf_floats, stream)
 
 
 def rms_norm_rope(out, x, w, k, tokens, n_q_heads, n_kv_heads, head_dim, eps, positions, pos0,

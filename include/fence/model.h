@@ -35,7 +35,7 @@ typedef struct {
 enum {
     FENCE_SEQUENCE_FUSED = 0,     /* q/k/v in one launch that also computes its input
                                      norm, gate/up + SwiGLU (and its norm) in another;
-                                     QK-norm + RoPE + KV store in one */
+                                     QK-norm + RoPE + KV store inside attention */
     FENCE_SEQUENCE_REFERENCE = 1  /* the launch order of src/model/qwen3.cu:267-341 */
 };
 

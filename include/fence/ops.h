@@ -225,6 +225,25 @@ int fence_qk_norm_rope_store_kv(float* q, float* k, const float* v,
                                 int pos0, float freq_base, int style,
                                 hipStream_t stream);
 
+/* One decode token's attention block from its unprepared q, k and v
+ * (src/model/qwen3.cu:292-308): fence_qk_norm_rope_store_kv for the token at
+ * position pos (one token), then fence_gqa_attention_f16 over seq_len =
+ * pos + 1 -- the same outputs and cache rows, bit for bit.  With head_dim
+ * 128 and 16-byte aligned operands it is one attention launch (plus the merge
+ * of its splits): every workgroup applies QK-norm and RoPE to its own q heads,
+ * and the ones that attend to position pos prepare its k and v themselves
+ * and write the cache row; otherwise it makes the two calls.  q and k are
+ * inputs that may be overwritten (the two calls leave the prepared values
+ * there; the one launch leaves them as they were).  style:
+ * FENCE_ROPE_NEOX or FENCE_ROPE_INTERLEAVED. */
+int fence_gqa_attention_qk_f16(float* attn_out, void* out_f16, float* q, float* k,
+                               const float* v, const float* q_norm_w,
+                               const float* k_norm_w, void* k_cache, void* v_cache,
+                               int head_dim, int n_q_heads, int n_kv_heads, int pos,
+                               int max_ctx, float eps, float freq_base, int style,
+                               float* score_buf, int64_t score_buf_floats,
+                               hipStream_t stream);
+
 /* out_t = RoPE(rms_norm(x_t, w)) for x [tokens][n_q_heads*head_dim],
  * w [n_q_heads*head_dim], the normalised row viewed as n_q_heads heads; k
  * (may be NULL) gets RoPE only.  out may equal x. */

@@ -104,7 +104,7 @@ struct ScratchBuffers {
 /* The kernel sequence forward() launches. */
 enum class Qwen3Sequence {
     Fused,      // layer-boundary norms inside the q/k/v and gate/up launches, q/k/v, QK-norm +
-                // RoPE + KV store, attention + conversion, gate/up + SwiGLU: 7 calls per layer
+                // RoPE + KV store inside attention (+ conversion), gate/up + SwiGLU: 6 calls per layer
     Reference,  // the reference's launcher order, src/model/qwen3.cu:267-341
 };
 

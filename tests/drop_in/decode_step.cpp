@@ -209,10 +209,8 @@ void layer_fused(const Layer& L, Scratch& s, int pos, hipStream_t st) {
     const fence_rms_input attn_in{s.hidden, s.tmp, s.residual, L.attn_norm, s.x_half, EPS};
     fence_gemv_q6k_multi_rms(3, w_qkv, y_qkv, nullptr, m_qkv, &attn_in, E, st);
     std::swap(s.hidden, s.residual);
-    fence_qk_norm_rope_store_kv(s.q, s.k, s.v, L.q_norm, L.k_norm, L.kc, L.vc, CTX, 1, NQ, NKV, HD, EPS, nullptr, pos,
-                                BASE, FENCE_ROPE_NEOX, st);
-    fence_gqa_attention_f16(nullptr, s.x_half, s.q, L.kc, L.vc, HD, NQ, NKV, pos + 1, CTX, s.score_buf,
-                            4 * int64_t(NQ) * CTX, st);
+    fence_gqa_attention_qk_f16(nullptr, s.x_half, s.q, s.k, s.v, L.q_norm, L.k_norm, L.kc, L.vc, HD, NQ, NKV, pos, CTX,
+                               EPS, BASE, FENCE_ROPE_NEOX, s.score_buf, 4 * int64_t(NQ) * CTX, st);
     fence_gemv_q6k(L.wo, s.x_half, s.tmp, E, QD, st);
     const fence_rms_input ffn_in{s.hidden, s.tmp, s.residual, L.ffn_norm, s.x_half, EPS};
     fence_gemv_q6k_swiglu_rms_f16(L.wg, L.wu, &ffn_in, s.act_half, nullptr, FF, E, st);

@@ -159,3 +159,96 @@ def test_qk_norm_rope_store_kv_device_positions_skip_out_of_range():
     ref = run_separate(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, 0, 1e6, F.ROPE_NEOX)
     assert np.array_equal(got[2], ref[2]) and np.array_equal(got[3], ref[3])
     assert np.array_equal(got[1].view(np.uint32), ref[1].view(np.uint32))
+
+
+def attention_qk_operands(rng, nq, nkv, hd, ctx, norm):
+    q = rng.standard_normal((nq, hd)).astype(np.float32)
+    k = rng.standard_normal((nkv, hd)).astype(np.float32)
+    v = rng.standard_normal((nkv, hd)).astype(np.float32)
+    wq = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+    wk = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+    kc, vc = caches(rng, ctx, nkv * hd)
+    return q, k, v, wq, wk, kc, vc
+
+
+def run_attention_qk(ops, nq, nkv, hd, pos, base, style, ws_floats, fused):
+    """fused: fence_gqa_attention_qk_f16; else qk_norm_rope_store_kv then
+    gqa_attention_f16.  Returns (fp32 out, binary16 out, k cache, v cache)."""
+    torch = torch_mod()
+    q, k, v, wq, wk, kc, vc = ops
+    ctx = kc.shape[0]
+    qd, kd, vd = dev(q), dev(k), dev(v)
+    kcd, vcd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    wqp = None if wq is None else dev(wq).data_ptr()
+    wkp = None if wk is None else dev(wk).data_ptr()
+    ws = torch.empty(max(ws_floats, nq * ctx), dtype=torch.float32, device="cuda")
+    o32 = torch.full((nq * hd,), float("nan"), dtype=torch.float32, device="cuda")
+    o16 = torch.full((nq * hd,), -1, dtype=torch.int16, device="cuda")
+    LIVE.extend([ws, o32, o16])
+    if fused:
+        F.gqa_attention_qk_f16(o32.data_ptr(), o16.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), wqp, wkp,
+                               kcd.data_ptr(), vcd.data_ptr(), hd, nq, nkv, pos, ctx, 1e-6, base, style,
+                               ws.data_ptr(), ws_floats, stream())
+    else:
+        F.qk_norm_rope_store_kv(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), wqp, wkp, kcd.data_ptr(),
+                                vcd.data_ptr(), ctx, 1, nq, nkv, hd, 1e-6, None, pos, base, style, stream())
+        F.gqa_attention_f16(o32.data_ptr(), o16.data_ptr(), qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), hd, nq,
+                            nkv, pos + 1, ctx, ws.data_ptr(), ws_floats, stream())
+    return host(o32), host(o16).view(np.uint16), host(kcd).view(np.uint16), host(vcd).view(np.uint16)
+
+
+@pytest.mark.parametrize("nq,nkv,hd,pos,ctx,norm,style,wsmul", [
+    (32, 8, 128, 2915, 4096, True, F.ROPE_NEOX, 4),    # Qwen3-4B decode step, the model's workspace
+    (32, 8, 128, 2915, 4096, True, F.ROPE_NEOX, 1),    # the reference's score_buf size
+    (32, 8, 128, 0, 4096, True, F.ROPE_NEOX, 4),       # first position: one key, the new one
+    (32, 8, 128, 64, 4096, True, F.ROPE_NEOX, 4),      # 65 keys: pos alone at a split's end
+    (32, 8, 128, 4095, 4096, True, F.ROPE_NEOX, 4),    # the last cache row
+    (32, 8, 128, 700, 4096, False, F.ROPE_NEOX, 4),    # no QK-norm weights: RoPE only
+    (32, 8, 128, 333, 512, True, F.ROPE_INTERLEAVED, 1),
+    (8, 8, 128, 300, 512, True, F.ROPE_NEOX, 1),       # MHA: one head per workgroup
+    (12, 4, 128, 200, 512, True, F.ROPE_NEOX, 1),      # groups of 3: a workgroup with one head
+    (16, 4, 64, 100, 512, True, F.ROPE_NEOX, 1),       # head_dim 64: the two calls
+])
+def test_attention_qk_equals_head_ops_then_attention(oracle, nq, nkv, hd, pos, ctx, norm, style, wsmul):
+    rng = np.random.default_rng(pos + nq + hd + wsmul)
+    ops = attention_qk_operands(rng, nq, nkv, hd, ctx, norm)
+    ws_floats = wsmul * nq * ctx
+    got = run_attention_qk(ops, nq, nkv, hd, pos, 1e6, style, ws_floats, fused=True)
+    ref = run_attention_qk(ops, nq, nkv, hd, pos, 1e6, style, ws_floats, fused=False)
+    for g, r, what in zip(got, ref, ("fp32 out", "binary16 out", "k cache", "v cache")):
+        assert np.array_equal(g.view(np.uint32 if g.dtype == np.float32 else np.uint16),
+                              r.view(np.uint32 if r.dtype == np.float32 else np.uint16)), what
+    if pos == 2915 and wsmul == 1:  # and the oracle's chain, at the attention bar
+        q, k, v, wq, wk, kc, vc = ops
+        rq, rk = oracle.qk_norm_rope(q[None], k[None], wq, wk, 1e-6, None, pos, 1e6, style)
+        rkc, rvc = oracle.store_kv(kc, vc, rk.reshape(-1), v.reshape(-1), pos)
+        ref_o = oracle.gqa_attention(rq.reshape(-1), rkc, rvc, nq, nkv, hd, pos + 1).reshape(nq, hd)
+        V = np.abs(rvc[:pos + 1].view(np.float16).astype(np.float64).reshape(-1, nkv, hd))
+        gq = got[0].reshape(nq, hd).astype(np.float64)
+        for h in range(nq):
+            assert np.max(np.abs(gq[h] - ref_o[h])) <= 1e-5 * V[:, h // (nq // nkv), :].max() + 2e-6, f"head {h}"
+
+
+def test_attention_qk_rejects_bad_arguments():
+    torch = torch_mod()
+    nq, nkv, hd, ctx = 8, 2, 128, 64
+    b = torch.zeros(65536, dtype=torch.float32, device="cuda")
+    LIVE.append(b)
+    p = b.data_ptr()
+    L = F.lib()
+    args = [None, p, p + 4096, p + 8192, p + 12288, p + 16384, p + 16896, p + 17408, p + 25600, hd, nq, nkv, 5, ctx,
+            1e-6, 1e6, F.ROPE_NEOX, p + 33792, 0, stream()]
+
+    def st(**kw):
+        a = list(args)
+        for key, val in kw.items():
+            a[{"out16": 1, "wk": 6, "pos": 12, "style": 16, "ws_floats": 18}[key]] = val
+        return L.fence_gqa_attention_qk_f16(*a)
+
+    assert st(out16=None) == F.EINVAL
+    assert st(wk=None) == F.EINVAL        # one norm weight only
+    assert st(pos=ctx) == F.EINVAL        # past the cache
+    assert st(pos=-1) == F.EINVAL
+    assert st(style=7) == F.EINVAL
+    assert st(ws_floats=-1) == F.EINVAL
+    torch.cuda.synchronize()
