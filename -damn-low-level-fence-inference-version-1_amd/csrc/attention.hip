@@ -652,10 +652,20 @@ extern "C" int fence_gqa_attention_qk_f16(float* attn_out, void* out_f16, float*
     if (style != kRopeNeox && style != kRopeInter) return FENCE_ERROR_INVALID_VALUE;
     if (score_buf_floats == 0) score_buf_floats = static_cast<int64_t>(n_q_heads) * max_ctx;
     uint16_t* o16 = static_cast<uint16_t*>(out_f16);
-    const bool fused = head_dim == 128 && n_q_heads % n_kv_heads == 0 && freq_base > 0.0f && std::isfinite(freq_base) &&
-                       aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(k_cache, 16) &&
-                       aligned(v_cache, 16) && (!q_norm_w || (aligned(q_norm_w, 16) && aligned(k_norm_w, 16))) &&
-                       (!attn_out || aligned(attn_out, 4)) && aligned(o16, 2) && (!score_buf || aligned(score_buf, 4));
+    // Everything either call would reject is rejected here, before any work:
+    // an error never leaves q, k or the caches half updated.
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 2 * kMaxHalf || n_q_heads % n_kv_heads != 0 ||
+        !(freq_base > 0.0f) || !std::isfinite(freq_base))
+        return FENCE_ERROR_INVALID_VALUE;
+    if (!aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4) || !aligned(k_cache, 2) || !aligned(v_cache, 2) ||
+        (q_norm_w && (!aligned(q_norm_w, 4) || !aligned(k_norm_w, 4))) || (attn_out && !aligned(attn_out, 4)) ||
+        !aligned(o16, 2) || (score_buf && !aligned(score_buf, 4)))
+        return FENCE_ERROR_INVALID_VALUE;
+    const bool vec_attention = head_dim == 128 && aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16);
+    if (!vec_attention && (!score_buf || score_buf_floats < static_cast<int64_t>(n_q_heads) * max_ctx))
+        return FENCE_ERROR_INVALID_VALUE;  // the generic kernel keeps every score in score_buf
+    const bool fused = vec_attention && aligned(k, 16) && aligned(v, 16) &&
+                       (!q_norm_w || (aligned(q_norm_w, 16) && aligned(k_norm_w, 16)));
     if (!fused) {  // the two calls it stands for
         if (int st = fence_qk_norm_rope_store_kv(q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, max_ctx, 1, n_q_heads,
                                                  n_kv_heads, head_dim, eps, nullptr, pos, freq_base, style, stream))

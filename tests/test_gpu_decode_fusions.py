@@ -252,3 +252,24 @@ def test_attention_qk_rejects_bad_arguments():
     assert st(style=7) == F.EINVAL
     assert st(ws_floats=-1) == F.EINVAL
     torch.cuda.synchronize()
+
+
+def test_attention_qk_error_changes_nothing():
+    """head_dim 64 takes the two calls; a score_buf too small for the generic
+    attention is EINVAL up front: q, k and the caches are left as they were."""
+    torch = torch_mod()
+    nq, nkv, hd, ctx, pos = 8, 2, 64, 32, 7
+    rng = np.random.default_rng(12)
+    q, k, v, wq, wk, kc, vc = attention_qk_operands(rng, nq, nkv, hd, ctx, True)
+    qd, kd, kcd, vcd = dev(q), dev(k), dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    ws = torch.empty(nq * ctx - 1, dtype=torch.float32, device="cuda")
+    o16 = torch.empty(nq * hd, dtype=torch.int16, device="cuda")
+    LIVE.extend([ws, o16])
+    st = F.lib().fence_gqa_attention_qk_f16(None, o16.data_ptr(), qd.data_ptr(), kd.data_ptr(), dev(v).data_ptr(),
+                                            dev(wq).data_ptr(), dev(wk).data_ptr(), kcd.data_ptr(), vcd.data_ptr(),
+                                            hd, nq, nkv, pos, ctx, 1e-6, 1e6, F.ROPE_NEOX, ws.data_ptr(),
+                                            nq * ctx - 1, stream())
+    assert st == F.EINVAL
+    assert np.array_equal(host(qd).view(np.uint32), q.view(np.uint32))
+    assert np.array_equal(host(kd).view(np.uint32), k.view(np.uint32))
+    assert np.array_equal(host(kcd).view(np.uint16), kc) and np.array_equal(host(vcd).view(np.uint16), vc)
