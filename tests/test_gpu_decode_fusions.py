@@ -208,6 +208,10 @@ def run_attention_qk(ops, nq, nkv, hd, pos, base, style, ws_floats, fused):
     (8, 8, 128, 300, 512, True, F.ROPE_NEOX, 1),       # MHA: one head per workgroup
     (12, 4, 128, 200, 512, True, F.ROPE_NEOX, 1),      # groups of 3: a workgroup with one head
     (16, 4, 64, 100, 512, True, F.ROPE_NEOX, 1),       # head_dim 64: the two calls
+    (32, 8, 128, 63, 4096, True, F.ROPE_NEOX, 4),      # 64 keys: one split, one full sub-chunk
+    (32, 8, 128, 127, 4096, True, F.ROPE_NEOX, 4),     # 128 keys: two splits of 64
+    (32, 8, 128, 1023, 4096, True, F.ROPE_NEOX, 1),    # splits capped by the workspace
+    (32, 8, 128, 2047, 4096, False, F.ROPE_INTERLEAVED, 4),
 ])
 def test_attention_qk_equals_head_ops_then_attention(oracle, nq, nkv, hd, pos, ctx, norm, style, wsmul):
     rng = np.random.default_rng(pos + nq + hd + wsmul)

@@ -112,6 +112,17 @@ def test_multi_rms_equals_norm_then_gemv(Ms, K, residual):
     check_multi(Ws, Ms, K, hid, res, w)
 
 
+@pytest.mark.parametrize("K", [512, 768, 1024 + 256, 1536, 2048, 3072, 3584, 6144, 7936])
+def test_multi_rms_row_lengths(K):
+    """Row lengths of 2-31 blocks: every (PASSES, WPR) shape the prologue
+    runs in, T from 128 to 1024 threads, one and two float4 per lane."""
+    rng = np.random.default_rng(K)
+    Ms = (96, 32)
+    Ws = [make_q6k_matrix(rng, M, K) for M in Ms]
+    hid, res, w = row(rng, K)
+    check_multi(Ws, Ms, K, hid, res, w)
+
+
 @pytest.mark.parametrize("K,rows", [(2560, 40), (5120, 12)])
 def test_multi_rms_many_rows(K, rows):
     """Many rows through a small GEMV: the norm's order, element by element."""
@@ -145,7 +156,7 @@ def run_pair(Wg, Wu, M, K, hid, res, w, fp32=True):
 @pytest.mark.parametrize("M,K", [
     (9728, 2560),   # Qwen3-4B gate/up
     (14336, 4096),  # Llama-3-8B gate/up
-    (1000, 5120),   # two float4 per lane
+    (1000, 5120),   # two float4 per lane: a pair takes the two launches
     (40, 2560),
     (64, 9472),     # 37 blocks: the two-launch path
 ])
