@@ -102,10 +102,26 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
     __shared__ __align__(16) uint16_t kvn[QK ? 2 : 1][HD];      // prologue: position pos's k, v (binary16)
     const int group = n_q / n_kv;
     const int head_groups = (group + GT - 1) / GT;
-    const int kvh = blockIdx.x / head_groups;
-    const int h0 = kvh * group + (blockIdx.x % head_groups) * GT;  // first query head of this workgroup
-    const int ng = min(GT, kvh * group + group - h0);              // heads present (GT or fewer)
-    const int split = blockIdx.y;
+    // The head_groups workgroups of one (kv head, split) read the same K and V
+    // rows.  Workgroups are dispatched to the 8 XCDs round-robin by linear
+    // id, and each XCD has its own L2, so with n_kv a multiple of 8 the ids
+    // are remapped to put those workgroups 8 ids apart -- on one XCD, where
+    // the later reads hit the earlier ones' lines (measured: 12.5 -> 12.0 us
+    // at 2916 positions, 14.4 -> 13.7 us at 4096, split + merge).  The work of
+    // each workgroup, and so every result, is unchanged.
+    int bx = blockIdx.x, by = blockIdx.y;
+    if (head_groups > 1 && n_kv % 8 == 0) {
+        const int L = blockIdx.x + gridDim.x * blockIdx.y;
+        const int r = L >> 3;
+        const int P = (r / head_groups) * 8 + (L & 7);  // (kv head, split) = (P % n_kv, P / n_kv)
+        bx = (P % n_kv) * head_groups + r % head_groups;
+        by = P / n_kv;
+    }
+    const int kvh = bx / head_groups;
+    const int hgi = bx % head_groups;                        // head group within the kv head's
+    const int h0 = kvh * group + hgi * GT;                   // first query head of this workgroup
+    const int ng = min(GT, kvh * group + group - h0);        // heads present (GT or fewer)
+    const int split = by;
     const int t_begin = split * chunk;
     const int t_end = min(seq_len, t_begin + chunk);
     const int lane = threadIdx.x & 63;
@@ -269,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
                 st_h4<false>(&kvn[0][HALF + 4 * i], b);
                 st_h4<false>(&kvn[1][4 * i], va);
                 st_h4<false>(&kvn[1][HALF + 4 * i], vb);
-                if (blockIdx.x % head_groups == 0) {  // one writer per kv head
+                if (hgi == 0) {  // one writer per kv head
                     const int64_t at = static_cast<int64_t>(pos) * kv_dim + static_cast<int64_t>(kvh) * HD;
                     st_h4<false>(qk.kc + at + 4 * i, a);
                     st_h4<false>(qk.kc + at + HALF + 4 * i, b);
