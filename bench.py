@@ -155,37 +155,83 @@ def read_traffic(kernel_key: str):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(seconds: float):
-    """Scalar oracle on one host core over a bounded sample of the step."""
+CPU_ROWS = 64  # the CPU sample: 64 of the 512 token rows per op (same per-row shapes)
+
+
+def _cpu_sample(seed: int):
+    """One thread's operands and a function running the step's three ops on
+    them through the scalar oracle (the C library; ctypes drops the GIL)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_py import INTERLEAVED, Oracle, make_q8_0_table as np_table
 
     o = Oracle()
-    rng = np.random.default_rng(1)
-    rows = 64  # sample: 64 of the 512 token rows per op (same per-row shapes)
+    rng = np.random.default_rng(seed)
     vocab_sample = 4096  # the gather reads random rows; a smaller table keeps setup short
     table = np_table(rng, vocab_sample, HIDDEN)
-    ids = rng.integers(0, vocab_sample, rows).astype(np.int32)
-    x = rng.standard_normal((rows, HIDDEN)).astype(np.float32)
+    ids = rng.integers(0, vocab_sample, CPU_ROWS).astype(np.int32)
+    x = rng.standard_normal((CPU_ROWS, HIDDEN)).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(HIDDEN)).astype(np.float32)
-    k = rng.standard_normal((rows, NKV, HD)).astype(np.float32)
-    g = rng.standard_normal((rows, FFN)).astype(np.float32)
-    u = rng.standard_normal((rows, FFN)).astype(np.float32)
-    sample_bytes = STEP_BYTES * rows / T
-    reps, t0 = 0, time.perf_counter()
-    while True:
+    k = rng.standard_normal((CPU_ROWS, NKV, HD)).astype(np.float32)
+    g = rng.standard_normal((CPU_ROWS, FFN)).astype(np.float32)
+    u = rng.standard_normal((CPU_ROWS, FFN)).astype(np.float32)
+
+    def step():
         o.embed_q8_0_gather(table, vocab_sample, ids, HIDDEN)
         o.rms_norm_rope(x, w, k, NQ, HD, EPS, None, 0, THETA, INTERLEAVED)
         o.silu_mul(g, u)
+    return step
+
+
+def cpu_baseline(seconds: float):
+    """Scalar oracle on one host core over a bounded sample of the step."""
+    step = _cpu_sample(1)
+    sample_bytes = STEP_BYTES * CPU_ROWS / T
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        step()
         reps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
     return {"value": round(sample_bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": f"configs[1] step ops on {rows} of {T} token rows (same per-row shapes), "
+            "sample": f"configs[1] step ops on {CPU_ROWS} of {T} token rows (same per-row shapes), "
                       f"{reps} reps in {el:.1f} s, oracle incl. numpy wrapper copies"}
+
+
+def cpu_baseline_all_cores(seconds: float):
+    """The same oracle over rows on the host's cores: one thread per core of
+    the GPU box's share (at most 16), each running the step's ops on its own
+    64-row sample; value = all threads' bytes / wall time."""
+    import threading
+
+    n = max(1, min(16, os.cpu_count() or 1))
+    steps = [_cpu_sample(1 + i) for i in range(n)]
+    counts = [0] * n
+    start = threading.Barrier(n + 1)
+    t_end = [0.0]
+
+    def run(i):
+        start.wait()
+        while time.perf_counter() < t_end[0]:
+            steps[i]()
+            counts[i] += 1
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(n)]
+    for th in threads:
+        th.start()
+    t0 = time.perf_counter()
+    t_end[0] = t0 + seconds
+    start.wait()
+    for th in threads:
+        th.join()
+    el = time.perf_counter() - t0
+    sample_bytes = STEP_BYTES * CPU_ROWS / T
+    return {"value": round(sample_bytes * sum(counts) / el / 1e9, 4), "unit": "GB/s", "cores": n,
+            "kind": "port",
+            "sample": f"{n} threads, each the configs[1] step ops on its own {CPU_ROWS} token rows, "
+                      f"{sum(counts)} reps in {el:.1f} s"}
 
 
 def main():
@@ -294,6 +340,7 @@ def main():
     copy_gbps = copy_calibration(torch)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu_all = None if args.no_cpu else cpu_baseline_all_cores(args.cpu_seconds / 2)
     if args.all:
         all_configs(torch, F, args.all, args.all_reps)
 
@@ -325,6 +372,7 @@ def main():
         "decode_qwen3_4b": decode_model,
         "copy_calibration_GBps": copy_gbps,
         "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
         "wall_s_timed": round(wall, 4),
     }
     print(json.dumps(line), flush=True)
