@@ -1,0 +1,69 @@
+"""The GGUF reader (csrc/gguf.cpp, the host side of src/gguf/gguf_parser.cpp's
+role) built with AddressSanitizer and UndefinedBehaviorSanitizer (g++, host
+code only) and run over a valid file and 600 corruptions of it: random bit
+flips in the header, large little-endian integers written over header fields,
+truncations, and bytes appended past the data.  Every file must open with its
+tensors inside it or be rejected with BAD_FILE, and the sanitizers must report
+nothing (they abort the run on the first finding)."""
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from gguf_writer import ARRAY, F32, FLOAT32, INT32, Q6_K, Q8_0, STRING, UINT32, write_gguf
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "-damn-low-level-fence-inference-version-1_amd")
+
+
+def build(tmp_path):
+    exe = tmp_path / "gguf_walk"
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+           "-fno-omit-frame-pointer", f"-I{ROOT}/include", "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__",
+           os.path.join(PKG, "csrc", "gguf.cpp"), os.path.join(ROOT, "tests", "sanitize", "gguf_walk.cpp"),
+           "-o", str(exe)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=300)
+    return exe
+
+
+@pytest.mark.skipif(shutil.which("g++") is None or not os.path.isdir("/opt/rocm/include"),
+                    reason="needs g++ and the ROCm headers")
+def test_reader_under_sanitizers_on_corrupted_files(tmp_path):
+    exe = build(tmp_path)
+    good_path = tmp_path / "ok.gguf"
+    meta = [("general.architecture", STRING, "qwen3"), ("qwen3.block_count", UINT32, 2),
+            ("tok", ARRAY, (STRING, ["a", "bc", "def"])), ("f", FLOAT32, 0.5), ("n", ARRAY, (INT32, [1, 2, 3]))]
+    tensors = [("a", [64], F32, np.arange(64, dtype=np.float32).tobytes()),
+               ("b", [256, 2], Q6_K, bytes(2 * 210)), ("c", [32, 3], Q8_0, bytes(3 * 34))]
+    write_gguf(good_path, meta, tensors)
+    good = good_path.read_bytes()
+    rng = np.random.default_rng(77)
+    files = [str(good_path)]
+    for trial in range(600):
+        b = bytearray(good)
+        kind = trial % 4
+        if kind == 0:  # flip bits in a few bytes of the first 400 (header, metadata, tensor infos)
+            for i in rng.integers(0, min(400, len(b)), size=int(rng.integers(1, 5))):
+                b[i] ^= int(rng.integers(1, 256))
+        elif kind == 1:  # a large u64 over a header field
+            i = int(rng.integers(0, min(400, len(b)) - 8))
+            big = [2**63, 2**40, 2**32 - 1, 1 << 20, 2**64 - 1, 2**31][int(rng.integers(0, 6))]
+            b[i:i + 8] = big.to_bytes(8, "little")
+        elif kind == 2:  # truncate
+            b = b[:int(rng.integers(1, len(b)))]
+        else:  # a flip anywhere, plus trailing bytes
+            b[int(rng.integers(0, len(b)))] ^= 0xFF
+            b += bytes(int(rng.integers(1, 64)))
+        p = tmp_path / f"bad{trial}.gguf"
+        p.write_bytes(bytes(b))
+        files.append(str(p))
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:halt_on_error=1",
+               UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
+    env.pop("LD_PRELOAD", None)
+    r = subprocess.run([str(exe)] + files, capture_output=True, text=True, errors="replace", timeout=300, env=env)
+    assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-4000:])
+    assert "ERROR: AddressSanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-4000:]
+    opened = int(r.stdout.split("opened ")[1].split()[0])
+    assert opened >= 1  # the valid file at least
