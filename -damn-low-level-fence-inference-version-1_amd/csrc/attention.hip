@@ -571,7 +571,7 @@ int launch_split_qk(float* out, uint16_t* out16, float* ws, const float* q, cons
 }  // namespace
 
 // out (fp32) and/or out16 (its binary16 rounding, the f32_to_f16 of
-// src/model/qwen3.cu:308 fused) receive the result.
+// src/model/qwen3.cu:310 fused) receive the result.
 // ws holds ws_floats floats (the reference's score_buf: n_q * max_ctx).
 // qk (with style rope): q is unprepared and the launch applies QK-norm, RoPE
 // and the KV store of position seq_len - 1 itself; only on the vector path

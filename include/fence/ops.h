@@ -139,13 +139,13 @@ int fence_gqa_attention(float* attn_out, const float* q, const void* k_cache,
                         int n_kv_heads, int seq_len, int max_ctx, float* score_buf,
                         hipStream_t stream);
 
-/* Replaces store_kv, src/kernels/ops.cuh:434-443 (src/model/qwen3.cu:302):
+/* Replaces store_kv, src/kernels/ops.cuh:435-443 (src/model/qwen3.cu:303):
  * k_cache[pos][i] = binary16(k[i]), v_cache[pos][i] = binary16(v[i]), i <
  * kv_dim.  pos outside [0, max_ctx) is FENCE_ERROR_INVALID_VALUE. */
 int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v,
                    int pos, int kv_dim, int max_ctx, hipStream_t stream);
 
-/* Replaces argmax, src/kernels/ops.cuh:482-487 (greedy sampling):
+/* Replaces argmax, src/kernels/ops.cuh:465-505 (greedy sampling):
  * *result = index of the largest of x[0..n), the lowest such index on a tie;
  * NaN never wins; n == 0 gives 0. */
 int fence_argmax(const float* x, int* result, int n, hipStream_t stream);
@@ -194,7 +194,7 @@ int fence_qk_norm_rope(float* q, float* k, const float* q_norm_w,
                        int style, hipStream_t stream);
 
 /* fence_gqa_attention with its conversion for the o projection
- * (src/model/qwen3.cu:304-308: gqa_attention, then f32_to_f16 of attn_out)
+ * (src/model/qwen3.cu:305-310: gqa_attention, then f32_to_f16 of attn_out)
  * in the same launches: out_f16 [n_q_heads][head_dim] = binary16 of the
  * result; attn_out (fp32) may be NULL.  score_buf_floats is score_buf's size
  * in floats (0: the reference's n_q_heads * max_ctx).  A larger buffer lets
@@ -208,7 +208,7 @@ int fence_gqa_attention_f16(float* attn_out, void* out_f16, const float* q,
                             hipStream_t stream);
 
 /* fence_qk_norm_rope, then store_kv of the rotated k and of v, in one pass
- * (src/model/qwen3.cu:293-300): after the norm and RoPE of token t's q and k
+ * (src/model/qwen3.cu:292-303): after the norm and RoPE of token t's q and k
  * (both still written in fp32), its k and v [n_kv_heads*head_dim] are
  * written as binary16 into row pos_t of k_cache / v_cache
  * [max_ctx][n_kv_heads*head_dim] (store_kv, src/kernels/ops.cuh:419-443),
@@ -226,7 +226,7 @@ int fence_qk_norm_rope_store_kv(float* q, float* k, const float* v,
                                 hipStream_t stream);
 
 /* One decode token's attention block from its unprepared q, k and v
- * (src/model/qwen3.cu:292-308): fence_qk_norm_rope_store_kv for the token at
+ * (src/model/qwen3.cu:292-310): fence_qk_norm_rope_store_kv for the token at
  * position pos (one token), then fence_gqa_attention_f16 over seq_len =
  * pos + 1 -- the same outputs and cache rows, bit for bit.  With head_dim
  * 128 and 16-byte aligned operands it is one attention launch (plus the merge

@@ -95,13 +95,13 @@ inline void gqa_attention(float* attn_out, const float* q, const half* k_cache, 
                                              n_kv_heads, seq_len, max_ctx, score_buf, stream));
 }
 
-/* src/kernels/ops.cuh:434 */
+/* src/kernels/ops.cuh:435 */
 inline void store_kv(half* k_cache, half* v_cache, const float* k, const float* v, int pos,
                      int kv_dim, int max_ctx, hipStream_t stream = 0) {
     fence_detail::record(fence_store_kv(k_cache, v_cache, k, v, pos, kv_dim, max_ctx, stream));
 }
 
-/* src/kernels/ops.cuh:482 */
+/* src/kernels/ops.cuh:501 */
 inline void argmax(const float* x, int* result, int n, hipStream_t stream = 0) {
     fence_detail::record(fence_argmax(x, result, n, stream));
 }

@@ -120,7 +120,7 @@ def test_store_kv_bit_exact(oracle, pos, kv_dim):
 
 
 def test_store_then_attend(oracle):
-    """A decode step's order (qwen3.cu:302-305): store k, v at pos, attend over pos + 1."""
+    """A decode step's order (qwen3.cu:303-306): store k, v at pos, attend over pos + 1."""
     torch = torch_mod()
     n_q, n_kv, hd, ctx, pos = 32, 8, 128, 4096, 2915
     rng = np.random.default_rng(9)

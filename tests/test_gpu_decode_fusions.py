@@ -1,7 +1,7 @@
 """GPU checks of the decode-step fusions that replace two reference launches
 with one: fence_gqa_attention_f16 (gqa_attention + f32_to_f16,
-src/model/qwen3.cu:304-308) and fence_qk_norm_rope_store_kv
-(rms_norm_per_head x2 + apply_rope + store_kv, src/model/qwen3.cu:293-302).
+src/model/qwen3.cu:305-310) and fence_qk_norm_rope_store_kv
+(rms_norm_per_head x2 + apply_rope + store_kv, src/model/qwen3.cu:292-303).
 
 The bar is bit equality with the separate entry points on the same operands
 (each of which has its own oracle parity tests); one case per function is
