@@ -100,6 +100,26 @@ def test_reference_sequence_is_bit_identical(qwen3_file):
         assert np.array_equal(fused.view(np.uint32), refseq.view(np.uint32)) and g1 == g2
 
 
+def test_long_decode_is_bit_identical(qwen3_file):
+    """300 positions: attention splits the sequence (up to five 64-key
+    splits), the KV caches fill, and the stream alternates between its two
+    buffers 600 times -- every position's logits still equal the reference
+    sequence's.  Both sequences split the same way while the reference-sized
+    score_buf holds the splits (max_ctx / 130 of them: 15 here); past that the
+    fused sequence's larger workspace splits further and the two agree to the
+    attention bar instead, as at max_ctx 512 beyond 192 positions."""
+    path, _, _ = qwen3_file
+    rng = np.random.default_rng(11)
+    tokens = [int(t) for t in rng.integers(0, 1024, 300)]
+    with M.Model(path, max_ctx=2048) as m:
+        fused, g1 = decode(m, tokens, M.SEQUENCE_FUSED)
+        refseq, g2 = decode(m, tokens, M.SEQUENCE_REFERENCE)
+    assert np.all(np.isfinite(fused))
+    diff = np.flatnonzero(np.any(fused.view(np.uint32) != refseq.view(np.uint32), axis=1))
+    assert diff.size == 0, f"positions differing: {diff[:10]}"
+    assert g1 == g2
+
+
 def test_qwen2_style_file(oracle, tmp_path):
     """No QK-norm, q/k/v biases, and no key_length / rope / epsilon keys:
     the reference's fallbacks (src/model/qwen3.cu:141-176) apply."""
