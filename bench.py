@@ -183,6 +183,18 @@ def _cpu_sample(seed: int):
     return step
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo ("unknown" elsewhere)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds: float):
     """Scalar oracle on one host core over a bounded sample of the step."""
     step = _cpu_sample(1)
@@ -195,7 +207,7 @@ def cpu_baseline(seconds: float):
         if el >= seconds:
             break
     return {"value": round(sample_bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port",
+            "kind": "port", "cpu": _cpu_model(),
             "sample": f"configs[1] step ops on {CPU_ROWS} of {T} token rows (same per-row shapes), "
                       f"{reps} reps in {el:.1f} s, oracle incl. numpy wrapper copies"}
 
@@ -229,7 +241,7 @@ def cpu_baseline_all_cores(seconds: float):
     el = time.perf_counter() - t0
     sample_bytes = STEP_BYTES * CPU_ROWS / T
     return {"value": round(sample_bytes * sum(counts) / el / 1e9, 4), "unit": "GB/s", "cores": n,
-            "kind": "port",
+            "kind": "port", "cpu": _cpu_model(),
             "sample": f"{n} threads, each the configs[1] step ops on its own {CPU_ROWS} token rows, "
                       f"{sum(counts)} reps in {el:.1f} s"}
 
