@@ -45,6 +45,11 @@
 #ifndef FENCE_GEMV_Q6K_RESIDENT
 #define FENCE_GEMV_Q6K_RESIDENT 1
 #endif
+// Launches of at most this many rows of 13-16 blocks take the four-wave form
+// of the one-wave layout (XW below; same results, bit for bit).
+#ifndef FENCE_GEMV_Q6K_XW_ROWS
+#define FENCE_GEMV_Q6K_XW_ROWS 8192
+#endif
 
 namespace fence {
 namespace {
@@ -89,9 +94,13 @@ __device__ __forceinline__ float q6_col_bias(uint32_t x01, uint32_t x23) {
 }
 
 // d * sum_c sc_c * sum_k (q - 32) * x over the lane's 16 weights of one block,
-// each pair of weights one v_dot2c_f32_f16.
+// each pair of weights one v_dot2c_f32_f16.  Contraction off: the product
+// d * acc is rounded on its own and never fused into the caller's sum, so
+// every kernel layout that adds the same lane values in the same order gets
+// the same bits.
 __device__ __forceinline__ float q6_lane_dot(const Q6Lane& q, const uint32_t* xh, const float* kb, const int* sc,
                                              float d) {
+#pragma clang fp contract(off)
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -195,9 +204,16 @@ constexpr int staged_waves() { return PAIR && WPR == 4 ? 8 : 4; }
 // are gate rows and the second half the same rows of up.  NORM: x from
 // `rin` (see RmsIn), staged through the same LDS before the first group's
 // blocks are; NORM (1 or 2) is the norm kernel's float4s per lane, rin.vpt.
-template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM>
+// XW (with PASSES 1, WPR 4, rows of 13-16 blocks): the one-wave layout
+// <4, 1> spread over four waves -- wave s takes pass s, blocks [4s, 4s + 4),
+// and its lanes' values meet in LDS, where wave 0 adds each lane's four in
+// pass order before the wave sum: the same additions as one wave doing four
+// passes, so the rows are bit-identical to <4, 1>'s, computed by four times
+// as many waves.
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
+    static_assert(!XW || (PASSES == 1 && WPR == 4 && !PAIR && NORM == 0), "XW: <1, 4>, plain rows");
     constexpr int NW = staged_waves<WPR, PAIR>();
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
@@ -213,6 +229,7 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
     __shared__ __align__(16) uint8_t lds[kLdsBytes];
     __shared__ float red[NW];
     __shared__ float nred[NORM ? 16 : 1];  // the row norm's wave sums (T <= 1024)
+    __shared__ float xr[XW ? NW : 1][kWave];  // XW: each wave's lane values
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));  // wave-uniform
     const int seg = wid % WPR;
@@ -220,7 +237,12 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
     uint8_t* buf = lds + wid * kBufBytes;
     const int bslot = lane >> 4, h = (lane >> 3) & 1, j = lane & 7;
     int b0, b1;
-    segment(nb, seg, WPR, &b0, &b1);
+    if constexpr (XW) {
+        b0 = 4 * seg;  // nb > 12: every wave has at least one block
+        b1 = b0 + 4 < nb ? b0 + 4 : nb;
+    } else {
+        segment(nb, seg, WPR, &b0, &b1);
+    }
     const int64_t row_bytes = static_cast<int64_t>(nb) * kBlockBytes;
     const int64_t n_out = PAIR ? job.end[0] : job.end[job.n - 1];  // rows (PAIR: output rows)
 
@@ -415,9 +437,25 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
                 const float v = q6_lane_dot(q6_unpack(a, bq, c), xh[p], kb[p], sc, d);
                 part += on[p] ? v : 0.0f;
             }
-            part = wave_sum(part);
+            if constexpr (!XW) part = wave_sum(part);
         }
-        if constexpr (!PAIR && WPR == 1) {
+        if constexpr (XW) {
+            // one row per group (valid for all four waves): lane values of
+            // passes 0..3 in LDS, then wave 0's sum in pass order
+            xr[wid][lane] = part;
+            __syncthreads();
+            if (wid == 0) {
+                float t = 0.0f;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) t += xr[w][lane];
+                t = wave_sum(t);
+                if (lane == 0) {
+                    const float* bm = job.bias[m];
+                    job.y[m][lr] = bm ? t + bm[lr] : t;
+                }
+            }
+            __syncthreads();  // xr is rewritten by the next group
+        } else if constexpr (!PAIR && WPR == 1) {
             if (valid && lane == 0) {
                 const float* bm = job.bias[m];
                 job.y[m][lr] = bm ? part + bm[lr] : part;
@@ -548,12 +586,12 @@ int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t gro
     return launch(kernel, dim3(grid), dim3(threads), 0, s, args...);
 }
 
-template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM>
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
 int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
     static std::atomic<int> cache[64];
     constexpr int nw = staged_waves<WPR, PAIR>();
     constexpr int out_per_group = PAIR ? nw / WPR / 2 : nw / WPR;
-    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM>, kWave * nw, cache,
+    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW>, kWave * nw, cache,
                        (n_out + out_per_group - 1) / out_per_group, s, job, x, nb, rin);
 }
 
@@ -640,6 +678,11 @@ int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s, co
     if (pair)
         return staged ? launch_nb<true, false, 0>(job, n_out, x, nb, none, s) : launch_direct<true>(job, n_out, x, nb, s);
     if (!staged) return launch_direct<false>(job, n_out, x, nb, s);
+    // Few rows of 13-16 blocks: one wave per row leaves most SIMDs idle, so
+    // the one-wave layout runs spread over four waves per row (bit-identical).
+    if (FENCE_GEMV_Q6K_SPLIT == 0 && nb > 12 && nb <= 16 && n_out <= FENCE_GEMV_Q6K_XW_ROWS)
+        return job.n > 1 ? launch_staged<1, 4, false, true, 0, true>(job, n_out, x, nb, none, s)
+                         : launch_staged<1, 4, false, false, 0, true>(job, n_out, x, nb, none, s);
     return job.n > 1 ? launch_nb<false, true, 0>(job, n_out, x, nb, none, s)
                      : launch_nb<false, false, 0>(job, n_out, x, nb, none, s);
 }

@@ -198,6 +198,36 @@ def test_gemv_q6k_multi_equals_separate_launches(oracle, shapes, K):
         assert_close(got[i], oracle.gemv_q6k(W, x), abs_scale(W, x, K), f"multi {i}")
 
 
+BIG_ROWS = 8200  # more rows than the four-wave form takes (8192)
+
+
+@pytest.mark.parametrize("K", [3328, 3584, 3840, 4096])
+@pytest.mark.parametrize("M", [8, 256, 2560])
+def test_few_long_rows_equal_the_one_wave_layout(oracle, K, M):
+    """Launches of at most 8192 rows of 13-16 blocks run the one-wave layout
+    spread over four waves per row; a multi launch with a second matrix of
+    BIG_ROWS rows runs the one-wave layout itself.  Every row must agree bit
+    for bit, biased or not, including x of mixed magnitudes and an all-zero
+    x."""
+    rng = np.random.default_rng(K + M)
+    W = make_q6k_matrix(rng, M, K)
+    big = make_q6k_matrix(rng, BIG_ROWS, K)
+    b = rng.standard_normal(M).astype(np.float32)
+    mag = np.exp(rng.uniform(-6, 6, K))
+    xs = [rand_x(rng, K), (rng.standard_normal(K) * mag).astype(np.float16).view(np.uint16),
+          np.zeros(K, np.uint16)]
+    for i, x in enumerate(xs):
+        few = run_q6k(W, x, M, K)
+        many = run_q6k_multi([W, big], x, [M, BIG_ROWS], K)[0]
+        if i == 0:
+            assert_close(few, oracle.gemv_q6k(W, x), abs_scale(W, x, K), "few long rows")
+        assert np.array_equal(few.view(np.uint32), many.view(np.uint32)), \
+            f"{int((few.view(np.uint32) != many.view(np.uint32)).sum())} rows differ"
+        fb = run_q6k(W, x, M, K, b)
+        mb = run_q6k_multi([W, big], x, [M, BIG_ROWS], K, [b, None])[0]
+        assert np.array_equal(fb.view(np.uint32), mb.view(np.uint32))
+
+
 def test_gemv_q6k_multi_biases(oracle):
     K = 2560
     rng = np.random.default_rng(21)
