@@ -534,10 +534,11 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
     const int group = n_q / n_kv;
     const int head_groups = (group + GT - 1) / GT;
     const int base_wg = n_kv * head_groups;
-    // splits: enough workgroups to fill the GPU, at least 64 positions each,
-    // and no more partials than score_buf holds
+    // splits: enough workgroups to fill the GPU, at least one sub-chunk of
+    // positions each, and no more partials than score_buf holds
+    constexpr int kSubPositions = (kThreads / 16) * FENCE_ATTN_PPG;
     int64_t splits = (FENCE_ATTN_TARGET_WG + base_wg - 1) / base_wg;
-    const int64_t by_len = (seq_len + 63) / 64;
+    const int64_t by_len = (seq_len + kSubPositions - 1) / kSubPositions;
     if (splits > by_len) splits = by_len;
     const int64_t by_ws = ws ? ws_floats / (static_cast<int64_t>(n_q) * (HD + 2)) : 1;
     if (splits > by_ws) splits = by_ws;
