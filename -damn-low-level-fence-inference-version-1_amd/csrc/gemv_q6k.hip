@@ -441,7 +441,9 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_
         }
         if constexpr (XW) {
             // one row per group (valid for all four waves): lane values of
-            // passes 0..3 in LDS, then wave 0's sum in pass order
+            // passes 0..3 in LDS, then wave 0's sum in pass order.  Wave w's
+            // value is 0 + term w; t starts at +0 and never becomes -0, so
+            // t + (0 + term) == t + term bit for bit, as in the one-wave loop.
             xr[wid][lane] = part;
             __syncthreads();
             if (wid == 0) {
