@@ -153,3 +153,33 @@ def test_argmax(oracle, n, off):
     LIVE.append(r)
     F.argmax(xd.data_ptr() + 4 * off, r.data_ptr(), n, stream())
     assert int(host(r)[0]) == oracle.argmax(x[off:off + n])
+
+
+@pytest.mark.parametrize("n", [151936, 1027])
+@pytest.mark.parametrize("pattern", ["equal", "spread_ties", "tail_max", "last", "neg_inf", "nan", "below_init"])
+def test_argmax_patterns(oracle, n, pattern):
+    """Orders the workgroup's reduction must not change: ties spread over
+    many threads and waves (the lowest index wins), the maximum in the scalar
+    tail or at the end, and rows no value of which beats the initial -1e30
+    (index 0, as the reference's loop gives)."""
+    torch = torch_mod()
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32)
+    if pattern == "equal":
+        x[:] = 1.5
+    elif pattern == "spread_ties":
+        x[rng.choice(n, 40, replace=False)] = 9.0
+    elif pattern == "tail_max":
+        x[n - 2] = 9.0   # n % 4 == 3 for 1027: a scalar-tail element
+    elif pattern == "last":
+        x[n - 1] = 9.0
+    elif pattern == "neg_inf":
+        x[:] = -np.inf
+    elif pattern == "nan":
+        x[:] = np.nan
+    else:
+        x[:] = -1e35
+    r = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    LIVE.append(r)
+    F.argmax(dev(x).data_ptr(), r.data_ptr(), n, stream())
+    assert int(host(r)[0]) == oracle.argmax(x)
