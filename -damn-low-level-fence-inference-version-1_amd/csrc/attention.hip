@@ -65,11 +65,13 @@ struct QkIn {
 };
 
 // Split kernel: grid (n_kv * head_groups, splits); HD = 128.  The workgroup
-// walks its positions in sub-chunks of kSub: (A) every 16-lane group scores
-// its positions for the GT heads into LDS, (B) one wave per head takes the
-// sub-chunk's maximum and exponentials (each computed once) and rescales the
-// running sum, (C) every lane accumulates p * v for its 8 dims.  The V rows
-// of a sub-chunk are loaded together with its K rows, before phase A.
+// walks its positions in sub-chunks of kSub (= 64): (A) every 16-lane group
+// scores its positions for the GT heads into LDS, (B) every wave takes each
+// head's sub-chunk maximum, exponentials and sum (lane t: position t; all
+// waves compute the same values) and rescales its running sum, (C) every lane
+// accumulates p * v for its 8 dims, p_t read from lane t.  One barrier per
+// sub-chunk, after (A): the score buffer alternates between two halves.  The
+// V rows of a sub-chunk are loaded together with its K rows, before phase A.
 // FINAL: one split, write the output; else write (m, l, o) partials to ws.
 // ROPE (kRopeNeox / kRopeInter): a prologue applies QK-norm and RoPE to the
 // workgroup's GT q heads with the head kernels' arithmetic (head_math.hpp),
@@ -94,8 +96,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
     constexpr bool QK = ROPE != kRopeNone;
     constexpr int kUnits = G * (GT + 1);   // prologue: the GT q heads' units, then the k head's
     static_assert(!QK || (kThreads >= 3 * kWave && kUnits <= 2 * kWave), "prologue lanes");
-    __shared__ float sp[GT][kSub];         // scores, then weights p
-    __shared__ float hm[GT], hl[GT], hc[GT];
+    static_assert(kSub == kWave, "one position of a sub-chunk per lane in (B)");
+    __shared__ float sp[2][GT][kSub];      // scores of even / odd sub-chunks
     __shared__ __align__(16) float xo[kPG][GT][HD];
     __shared__ __align__(16) float qcs[QK ? HD : 1];            // prologue: cos[HALF] then sin[HALF]
     __shared__ __align__(16) float qs[QK ? GT : 1][HD];         // prologue: the prepared q heads
@@ -148,10 +150,14 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
     for (int g = 0; g < GT; ++g)
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
-    if (threadIdx.x < GT) {
-        hm[threadIdx.x] = -__builtin_inff();
-        hl[threadIdx.x] = 0.0f;
+    // running maximum and sum per head: every wave holds the same values
+    float hm[GT], hl[GT];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        hm[g] = -__builtin_inff();
+        hl[g] = 0.0f;
     }
+    int sub = 0;  // sub-chunks processed: sp[sub & 1] is this one's
 
     const uint16_t* kbase = kc + static_cast<int64_t>(kvh) * HD + 8 * sl;
     const uint16_t* vbase = vc + static_cast<int64_t>(kvh) * HD + 8 * sl;
@@ -183,6 +189,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
             }
         }
         // (A) scores, in log2 units
+        float(&spb)[GT][kSub] = sp[sub & 1];
 #pragma unroll
         for (int i = 0; i < kPPG; ++i) {
             float kf[8];
@@ -194,39 +201,37 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
 #pragma unroll
                 for (int k = 0; k < 8; ++k) d = __builtin_fmaf(qv[g][k], kf[k], d);
                 d = group_reduce<16>(d, OpAdd{});
-                if (sl == 0) sp[g][pg + kPG * i] = on[i] ? d * scale2 : -__builtin_inff();
+                if (sl == 0) spb[g][pg + kPG * i] = on[i] ? d * scale2 : -__builtin_inff();
             }
         }
+        // One barrier per sub-chunk: the next sub-chunk writes the other
+        // buffer, and the one after that comes after the next barrier.
         __syncthreads();
-        // (B) one wave per head: the sub-chunk's maximum, weights and sum
-        if (wave < GT) {
-            const int g = wave;
-            float m = -__builtin_inff();
-            for (int t = lane; t < kSub; t += 64) m = fmaxf(m, sp[g][t]);
-            m = wave_reduce(m, OpMax{});
-            const float mo = hm[g];
-            const float mn = fmaxf(mo, m);
-            float l = 0.0f;
-            for (int t = lane; t < kSub; t += 64) {
-                const float p = sp[g][t] == -__builtin_inff() ? 0.0f : exp2_hw(sp[g][t] - mn);
-                sp[g][t] = p;
-                l += p;
-            }
-            l = wave_reduce(l, OpAdd{});
-            if (lane == 0) {
-                const float c = hl[g] == 0.0f ? 0.0f : exp2_hw(mo - mn);  // nothing seen yet: no old weight
-                hl[g] = hl[g] * c + l;
-                hm[g] = mn;
-                hc[g] = c;
-            }
-        }
-        __syncthreads();
-        // (C) o = o * c + sum_t p_t v_t over the lane's dims
+        // (B) every wave, every head: lane t holds position t0 + t -- the
+        // sub-chunk's maximum, the weights and their sum, each computed the
+        // same way in every wave, so all waves keep the same running values
+        float pw[GT], cw[GT];
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
-            const float c = hc[g];
+            const float sv = spb[g][lane];
+            const float m = wave_reduce(fmaxf(-__builtin_inff(), sv), OpMax{});
+            const float mo = hm[g];
+            const float mn = fmaxf(mo, m);
+            const float p = sv == -__builtin_inff() ? 0.0f : exp2_hw(sv - mn);
+            float l = 0.0f;
+            l += p;
+            l = wave_reduce(l, OpAdd{});
+            const float c = hl[g] == 0.0f ? 0.0f : exp2_hw(mo - mn);  // nothing seen yet: no old weight
+            hl[g] = hl[g] * c + l;
+            hm[g] = mn;
+            cw[g] = c;
+            pw[g] = p;
+        }
+        // (C) o = o * c + sum_t p_t v_t over the lane's dims; p_t from lane t
 #pragma unroll
-            for (int k = 0; k < 8; ++k) o[g][k] *= c;
+        for (int g = 0; g < GT; ++g) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[g][k] *= cw[g];
         }
 #pragma unroll
         for (int i = 0; i < kPPG; ++i) {
@@ -235,12 +240,12 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
             for (int k = 0; k < 8; ++k) vf[k] = static_cast<float>(vr[i][k]);
 #pragma unroll
             for (int g = 0; g < GT; ++g) {
-                const float p = sp[g][pg + kPG * i];
+                const float p = __shfl(pw[g], pg + kPG * i, kWave);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) o[g][k] = __builtin_fmaf(p, vf[k], o[g][k]);
             }
         }
-        __syncthreads();  // sp and hc are rewritten by the next sub-chunk
+        ++sub;
     };
 
     if (t_begin < t_end) load_kv(t_begin);
@@ -325,7 +330,12 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         if (g >= ng) continue;
         float acc = 0.0f;
         for (int k = 0; k < kPG; ++k) acc += xo[k][g][d];
-        const float l = hl[g];
+        float l = hl[0], mg = hm[0];
+#pragma unroll
+        for (int k = 1; k < GT; ++k) {
+            l = g == k ? hl[k] : l;
+            mg = g == k ? hm[k] : mg;
+        }
         const int h = h0 + g;
         if constexpr (FINAL) {
             const float r = l == 0.0f ? 0.0f : acc / l;
@@ -335,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
             // partial of (head h, split): [m, l, o[HD]]
             float* p = ws + (static_cast<int64_t>(h) * gridDim.y + split) * (HD + 2);
             if (d == 0) {
-                p[0] = hm[g];
+                p[0] = mg;
                 p[1] = l;
             }
             p[2 + d] = acc;
