@@ -193,10 +193,16 @@ __device__ __forceinline__ int mat_of(const Q6Job& job, int64_t r, int64_t* lr) 
     return m;
 }
 
-// Waves of a staged workgroup: 4, or 8 for a gate/up pair whose rows take
-// four waves each.
-template <int WPR, bool PAIR>
-constexpr int staged_waves() { return PAIR && WPR == 4 ? 8 : 4; }
+// Waves of a staged workgroup: 4; 8 for a gate/up pair whose rows take four
+// waves each; 8 for a multi launch that normalises its input row in the
+// prologue with one wave per row.  Measured on MI355X for the last: every
+// workgroup computes the row norm, and two 8-wave workgroups per CU instead
+// of five 4-wave ones cut q/k/v from 9.04 to 7.28 us (K = 2560) and from
+// 10.44 to 9.40 us (K = 4096), p50; 6- and 12-wave workgroups were slower, and
+// so was 8 for the gate/up pair (15.24 -> 16.04 us).  A row's arithmetic
+// does not depend on the workgroup, so every result is the same.
+template <int WPR, bool PAIR, int NORM = 0>
+constexpr int staged_waves() { return NORM && !PAIR && WPR == 1 ? 8 : (PAIR && WPR == 4 ? 8 : 4); }
 
 // Staged kernel.  WPR waves per row (1, 2 or 4), each over at most 4 * PASSES
 // <= 16 blocks.  LDS: one buffer of kSegBytes per wave + red[].  A workgroup
@@ -211,10 +217,10 @@ constexpr int staged_waves() { return PAIR && WPR == 4 ? 8 : 4; }
 // passes, so the rows are bit-identical to <4, 1>'s, computed by four times
 // as many waves.
 template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
-__global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR>())) void gemv_q6k_staged_kernel(
+__global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
     static_assert(!XW || (PASSES == 1 && WPR == 4 && !PAIR && NORM == 0), "XW: <1, 4>, plain rows");
-    constexpr int NW = staged_waves<WPR, PAIR>();
+    constexpr int NW = staged_waves<WPR, PAIR, NORM>();
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
     constexpr int kChunkSlots = (kSegBytes / 16 + kWave - 1) / kWave;
@@ -591,7 +597,7 @@ int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t gro
 template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
 int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
     static std::atomic<int> cache[64];
-    constexpr int nw = staged_waves<WPR, PAIR>();
+    constexpr int nw = staged_waves<WPR, PAIR, NORM>();
     constexpr int out_per_group = PAIR ? nw / WPR / 2 : nw / WPR;
     return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW>, kWave * nw, cache,
                        (n_out + out_per_group - 1) / out_per_group, s, job, x, nb, rin);
