@@ -198,9 +198,11 @@ __device__ __forceinline__ int mat_of(const Q6Job& job, int64_t r, int64_t* lr) 
 // prologue with one wave per row.  Measured on MI355X for the last: every
 // workgroup computes the row norm, and two 8-wave workgroups per CU instead
 // of five 4-wave ones cut q/k/v from 9.04 to 7.28 us (K = 2560) and from
-// 10.44 to 9.40 us (K = 4096), p50; 6- and 12-wave workgroups were slower, and
-// so was 8 for the gate/up pair (15.24 -> 16.04 us).  A row's arithmetic
-// does not depend on the workgroup, so every result is the same.
+// 10.44 to 9.40 us (K = 4096), p50; 6-, 10- and 12-wave workgroups were
+// slower (a workgroup's waves spread over the CU's four SIMDs, so only
+// multiples of four fill it), and so was 8 for the gate/up pair (15.24 ->
+// 16.04 us).  A row's arithmetic does not depend on the workgroup, so every
+// result is the same.
 template <int WPR, bool PAIR, int NORM = 0>
 constexpr int staged_waves() { return NORM && !PAIR && WPR == 1 ? 8 : (PAIR && WPR == 4 ? 8 : 4); }
 
@@ -221,6 +223,7 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
     static_assert(!XW || (PASSES == 1 && WPR == 4 && !PAIR && NORM == 0), "XW: <1, 4>, plain rows");
     constexpr int NW = staged_waves<WPR, PAIR, NORM>();
+    static_assert(!XW || NW == WPR, "XW: one row per workgroup");
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
     constexpr int kChunkSlots = (kSegBytes / 16 + kWave - 1) / kWave;
