@@ -45,10 +45,16 @@
 #ifndef FENCE_GEMV_Q6K_RESIDENT
 #define FENCE_GEMV_Q6K_RESIDENT 1
 #endif
-// Launches of at most this many rows of 13-16 blocks take the four-wave form
-// of the one-wave layout (XW below; same results, bit for bit).
+// Launches of at most this many rows of 13-16 blocks take the one-wave layout
+// spread over FENCE_GEMV_Q6K_XW_WAVES (2 or 4) waves per row (XW below; same
+// results, bit for bit).  Measured on MI355X, p50: four waves per row run the
+// 2560 x 4096 o projection in 4.96 us against 5.36 with two (every row of it
+// then fits the GPU at once) and 6.00 with one.
 #ifndef FENCE_GEMV_Q6K_XW_ROWS
 #define FENCE_GEMV_Q6K_XW_ROWS 8192
+#endif
+#ifndef FENCE_GEMV_Q6K_XW_WAVES
+#define FENCE_GEMV_Q6K_XW_WAVES 4
 #endif
 
 namespace fence {
@@ -212,18 +218,17 @@ constexpr int staged_waves() { return NORM && !PAIR && WPR == 1 ? 8 : (PAIR && W
 // are gate rows and the second half the same rows of up.  NORM: x from
 // `rin` (see RmsIn), staged through the same LDS before the first group's
 // blocks are; NORM (1 or 2) is the norm kernel's float4s per lane, rin.vpt.
-// XW (with PASSES 1, WPR 4, rows of 13-16 blocks): the one-wave layout
-// <4, 1> spread over four waves -- wave s takes pass s, blocks [4s, 4s + 4),
-// and its lanes' values meet in LDS, where wave 0 adds each lane's four in
-// pass order before the wave sum: the same additions as one wave doing four
-// passes, so the rows are bit-identical to <4, 1>'s, computed by four times
-// as many waves.
+// XW (PASSES * WPR = 4, rows of 13-16 blocks): the one-wave layout <4, 1>
+// spread over WPR waves -- wave s takes passes PASSES*s .. PASSES*s +
+// PASSES - 1 (blocks from 4 * PASSES * s on), and each pass's lane values go
+// to LDS, where the row's first wave adds each lane's four in pass order
+// before the wave sum: the additions of one wave doing four passes, so the
+// rows are bit-identical to <4, 1>'s, computed by WPR times as many waves.
 template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
-    static_assert(!XW || (PASSES == 1 && WPR == 4 && !PAIR && NORM == 0), "XW: <1, 4>, plain rows");
+    static_assert(!XW || (PASSES * WPR == 4 && !PAIR && NORM == 0), "XW: four passes, plain rows");
     constexpr int NW = staged_waves<WPR, PAIR, NORM>();
-    static_assert(!XW || NW == WPR, "XW: one row per workgroup");
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
     constexpr int kChunkSlots = (kSegBytes / 16 + kWave - 1) / kWave;
@@ -238,7 +243,7 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
     __shared__ __align__(16) uint8_t lds[kLdsBytes];
     __shared__ float red[NW];
     __shared__ float nred[NORM ? 16 : 1];  // the row norm's wave sums (T <= 1024)
-    __shared__ float xr[XW ? NW : 1][kWave];  // XW: each wave's lane values
+    __shared__ float xr[XW ? NW : 1][XW ? PASSES : 1][kWave];  // XW: each pass's lane values
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));  // wave-uniform
     const int seg = wid % WPR;
@@ -247,8 +252,8 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
     const int bslot = lane >> 4, h = (lane >> 3) & 1, j = lane & 7;
     int b0, b1;
     if constexpr (XW) {
-        b0 = 4 * seg;  // nb > 12: every wave has at least one block
-        b1 = b0 + 4 < nb ? b0 + 4 : nb;
+        b0 = 4 * PASSES * seg;  // nb > 12: every wave has at least one block
+        b1 = b0 + 4 * PASSES < nb ? b0 + 4 * PASSES : nb;
     } else {
         segment(nb, seg, WPR, &b0, &b1);
     }
@@ -444,21 +449,21 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
                 const uint16_t dbits = *reinterpret_cast<const uint16_t*>(bb + p * kPassBytes + 208);
                 const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
                 const float v = q6_lane_dot(q6_unpack(a, bq, c), xh[p], kb[p], sc, d);
-                part += on[p] ? v : 0.0f;
+                if constexpr (XW) xr[wid][p][lane] = on[p] ? v : 0.0f;
+                else part += on[p] ? v : 0.0f;
             }
             if constexpr (!XW) part = wave_sum(part);
         }
         if constexpr (XW) {
-            // one row per group (valid for all four waves): lane values of
-            // passes 0..3 in LDS, then wave 0's sum in pass order.  Wave w's
-            // value is 0 + term w; t starts at +0 and never becomes -0, so
-            // t + (0 + term) == t + term bit for bit, as in the one-wave loop.
-            xr[wid][lane] = part;
+            // the row's first wave adds the lane values of passes 0..3 in
+            // order from 0, as the one-wave loop does, then the wave sum
             __syncthreads();
-            if (wid == 0) {
+            if (seg == 0 && valid) {
                 float t = 0.0f;
 #pragma unroll
-                for (int w = 0; w < NW; ++w) t += xr[w][lane];
+                for (int w = 0; w < WPR; ++w)
+#pragma unroll
+                    for (int p = 0; p < PASSES; ++p) t += xr[wid + w][p][lane];
                 t = wave_sum(t);
                 if (lane == 0) {
                     const float* bm = job.bias[m];
@@ -691,9 +696,13 @@ int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s, co
     if (!staged) return launch_direct<false>(job, n_out, x, nb, s);
     // Few rows of 13-16 blocks: one wave per row leaves most SIMDs idle, so
     // the one-wave layout runs spread over four waves per row (bit-identical).
-    if (FENCE_GEMV_Q6K_SPLIT == 0 && nb > 12 && nb <= 16 && n_out <= FENCE_GEMV_Q6K_XW_ROWS)
+    if (FENCE_GEMV_Q6K_SPLIT == 0 && nb > 12 && nb <= 16 && n_out <= FENCE_GEMV_Q6K_XW_ROWS) {
+        if constexpr (FENCE_GEMV_Q6K_XW_WAVES == 2)
+            return job.n > 1 ? launch_staged<2, 2, false, true, 0, true>(job, n_out, x, nb, none, s)
+                             : launch_staged<2, 2, false, false, 0, true>(job, n_out, x, nb, none, s);
         return job.n > 1 ? launch_staged<1, 4, false, true, 0, true>(job, n_out, x, nb, none, s)
                          : launch_staged<1, 4, false, false, 0, true>(job, n_out, x, nb, none, s);
+    }
     return job.n > 1 ? launch_nb<false, true, 0>(job, n_out, x, nb, none, s)
                      : launch_nb<false, false, 0>(job, n_out, x, nb, none, s);
 }
