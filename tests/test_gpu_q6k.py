@@ -228,6 +228,18 @@ def test_few_long_rows_equal_the_one_wave_layout(oracle, K, M):
         assert np.array_equal(fb.view(np.uint32), mb.view(np.uint32))
 
 
+def test_four_wave_threshold_is_invisible():
+    """8192 rows of 16 blocks take the four-wave form, 8200 rows the one-wave
+    layout: the shared rows agree bit for bit across the threshold."""
+    rng = np.random.default_rng(8192)
+    K = 4096
+    W = make_q6k_matrix(rng, BIG_ROWS, K)
+    x = rand_x(rng, K)
+    below = run_q6k(W[:8192], x, 8192, K)
+    above = run_q6k(W, x, BIG_ROWS, K)
+    assert np.array_equal(below.view(np.uint32), above[:8192].view(np.uint32))
+
+
 def test_gemv_q6k_multi_biases(oracle):
     K = 2560
     rng = np.random.default_rng(21)
