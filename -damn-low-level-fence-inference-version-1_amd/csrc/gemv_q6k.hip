@@ -46,15 +46,12 @@
 #define FENCE_GEMV_Q6K_RESIDENT 1
 #endif
 // Launches of at most this many rows of 13-16 blocks take the one-wave layout
-// spread over FENCE_GEMV_Q6K_XW_WAVES (2 or 4) waves per row (XW below; same
-// results, bit for bit).  Measured on MI355X, p50: four waves per row run the
-// 2560 x 4096 o projection in 4.96 us against 5.36 with two (every row of it
-// then fits the GPU at once) and 6.00 with one.
+// spread over four waves per row (XW below; same results, bit for bit).
+// Measured on MI355X, p50: the 2560 x 4096 o projection runs in 4.96 us with
+// four waves per row, 5.36 with two (two passes each, so every row of it fits
+// the GPU at once) and 6.00 with one.
 #ifndef FENCE_GEMV_Q6K_XW_ROWS
 #define FENCE_GEMV_Q6K_XW_ROWS 8192
-#endif
-#ifndef FENCE_GEMV_Q6K_XW_WAVES
-#define FENCE_GEMV_Q6K_XW_WAVES 4
 #endif
 
 namespace fence {
@@ -696,13 +693,9 @@ int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s, co
     if (!staged) return launch_direct<false>(job, n_out, x, nb, s);
     // Few rows of 13-16 blocks: one wave per row leaves most SIMDs idle, so
     // the one-wave layout runs spread over four waves per row (bit-identical).
-    if (FENCE_GEMV_Q6K_SPLIT == 0 && nb > 12 && nb <= 16 && n_out <= FENCE_GEMV_Q6K_XW_ROWS) {
-        if constexpr (FENCE_GEMV_Q6K_XW_WAVES == 2)
-            return job.n > 1 ? launch_staged<2, 2, false, true, 0, true>(job, n_out, x, nb, none, s)
-                             : launch_staged<2, 2, false, false, 0, true>(job, n_out, x, nb, none, s);
+    if (FENCE_GEMV_Q6K_SPLIT == 0 && nb > 12 && nb <= 16 && n_out <= FENCE_GEMV_Q6K_XW_ROWS)
         return job.n > 1 ? launch_staged<1, 4, false, true, 0, true>(job, n_out, x, nb, none, s)
                          : launch_staged<1, 4, false, false, 0, true>(job, n_out, x, nb, none, s);
-    }
     return job.n > 1 ? launch_nb<false, true, 0>(job, n_out, x, nb, none, s)
                      : launch_nb<false, false, 0>(job, n_out, x, nb, none, s);
 }
