@@ -1,29 +1,36 @@
 #!/usr/bin/env python3
 """Benchmark of the fused per-layer ops on one MI355X.
 
-Workload (Llama-3-8B-shaped prefill, T = 512):
-one step = the three fused ops of that config on seeded synthetic fp32 data
-  gather    fence_embed_q8_0_gather   512 ids from a 128256 x 4096 Q8_0 table
-  norm_rope fence_rms_norm_rope       x [512 x 4096] -> RMSNorm (eps 1e-5) ->
-                                      interleaved RoPE (theta 5e5, pos 0..511);
-                                      K [512 x 8 x 128] RoPE only
-  swiglu    fence_swiglu              gate, up [512 x 14336] -> out
+Headline workload: BASELINE.json configs[4], the largest configuration
+(Mixtral-8x7B-shaped attention/FFN elementwise stage, fp32).  One step runs
+its three ops on seeded synthetic data:
+  softmax  fence_softmax_causal  scores [32 x 2048 x 2048] in place, N(0,3) /
+                                 sqrt(128), keys k > q masked to -inf (masked
+                                 keys are never read and are written as exact
+                                 zeros)
+  swiglu   fence_swiglu          gate, up [8192 x 14336] ~ N(0,1) -> out
+  rope     fence_rope            interleaved, theta 1e6, Q [8192 x 32 x 128]
+                                 and K [8192 x 8 x 128] in place, positions
+                                 0..8191
 Throughput = algorithmic bytes (each input read once, each output written
-once) / time, as GB/s, with inputs resident in HBM.  Cold protocol: the step
-rotates over buffer sets totalling more than 1 GiB, so no step finds its data
-in the 256 MB Infinity Cache or the L2s.
+once; the causal softmax counts only the keys it reads) / time, as GB/s, with
+inputs resident in HBM.  Cold protocol: the step rotates over buffer sets of
+more than 1 GiB each, so no step finds its data in the 256 MB Infinity Cache
+or the L2s.
 
-Also reported: per-op kernel time and GB/s from passes right after the timed
-region that launch each op alone over the same cold rotation, every launch
-recording HIP events at its own kernel start and end
-(fence_time_next_launch -> hipExtLaunchKernel, on the launch stream: the
-interval a kernel-trace profiler reports); the roofline of the dominant
-kernel (swiglu) from K such launches;
-the Llama-3-8B decode-step op set in microseconds, the Q8_0 LM-head GEMV
-(128256 x 4096, once per decoded token), whole decode steps of a
-Qwen3-4B-shaped model through the GGUF loader and host forward, a device-copy
-calibration, and the CPU baseline (the scalar oracle on one host core,
-timed on a bounded sample of the same step).
+Also reported from the same run:
+  * per-op kernel time and GB/s of the step's ops, from passes right after the
+    timed region that launch each op alone over the same cold rotation, every
+    launch recording HIP events at its own kernel start and end
+    (fence_time_next_launch -> hipExtLaunchKernel, on the launch stream: the
+    interval a kernel-trace profiler reports); the roofline of the dominant
+    kernel (swiglu) from K such launches;
+  * the same per-op figures for every op of configs[0..3];
+  * the Llama-3-8B decode-step op set in microseconds, the Q8_0 LM-head GEMV,
+    whole decode steps of a Qwen3-4B-shaped model through the GGUF loader and
+    host forward, and a device-copy calibration;
+  * the CPU baseline: the scalar C oracle timed in C on the GPU box's host
+    cores over a bounded sample of the same step.
 """
 from __future__ import annotations
 
@@ -41,46 +48,49 @@ sys.path.insert(0, PKG)
 PEAK_HBM_GBPS = 8000.0
 METRIC = "achieved HBM GB/s and % of peak per fused op; µs per decode-step op set"
 
-# configs[1] shapes
-T = 512
-HIDDEN = 4096
+# configs[4] shapes
+SM_HEADS, SM_Q, SM_K = 32, 2048, 2048
+T4, FFN4 = 8192, 14336
 NQ, NKV, HD = 32, 8, 128
-FFN = 14336
-VOCAB = 128256
-EPS = 1e-5
-THETA = 5e5
+THETA4 = 1e6
 
-Q8_ROW = HIDDEN // 32 * 34
+SM_VALID = SM_HEADS * SM_Q * (SM_Q + 1) // 2  # keys a causal row reads (sq == sk)
 BYTES = {
-    # write T*HIDDEN fp32 + read T rows of the table + read T int32 ids
-    "gather": T * HIDDEN * 4 + T * Q8_ROW + T * 4,
-    # read x + write out + read w, plus K read + write
-    "norm_rope": 2 * T * NQ * HD * 4 + NQ * HD * 4 + 2 * T * NKV * HD * 4,
+    # read the unmasked keys, write every key
+    "softmax": 4 * SM_VALID + 4 * SM_HEADS * SM_Q * SM_K,
     # read gate + read up + write out
-    "swiglu": 3 * T * FFN * 4,
+    "swiglu": 3 * T4 * FFN4 * 4,
+    # read + write Q and K
+    "rope": 2 * T4 * (NQ + NKV) * HD * 4,
 }
 STEP_BYTES = sum(BYTES.values())
+SOFTMAX_GENERIC_BYTES = 2 * 4 * SM_HEADS * SM_Q * SM_K
 DOMINANT = "swiglu"
-KERNEL_NAMES = {"gather": "q8_gather_kernel", "norm_rope": "head_ops_vec_kernel",
-                "swiglu": "swiglu_vec_kernel"}
+KERNEL_NAMES = {"softmax": "softmax_vec_kernel", "swiglu": "swiglu_vec_kernel", "rope": "head_ops_vec_kernel"}
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "swiglu_config4_pmc.txt")
+
+# Llama-3-8B shapes (configs[1] and the decode-step op set)
+L3_HIDDEN, L3_FFN, L3_VOCAB, L3_THETA = 4096, 14336, 128256, 5e5
 
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--warm", action="store_true", help="reuse one buffer set (cache-warm)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--config-reps", type=int, default=20,
+                    help="launches per op of configs[0..3] (0 skips them)")
     ap.add_argument("--decode-reps", type=int, default=300)
     ap.add_argument("--decode-tokens", type=int, default=32,
                     help="tokens of the Qwen3-4B-shaped decode run (0 skips it)")
     ap.add_argument("--lm-head-reps", type=int, default=60,
                     help="launches of the Q8_0 LM-head GEMV pass (0 skips it)")
     ap.add_argument("--all", metavar="PATH", default=None,
-                    help="also measure every op of BASELINE.json configs[0..4] and write the "
-                         "per-op report (JSON) to PATH; a table goes to stderr")
+                    help="also measure the decode-path ops (GEMVs, attention, epilogues) of every "
+                         "config and write the per-op report (JSON) to PATH; a table goes to stderr")
     ap.add_argument("--all-reps", type=int, default=50)
     return ap.parse_args()
 
@@ -95,19 +105,24 @@ def make_q8_0_table(torch, gen, vocab, dim):
     return table
 
 
+def causal_scores(torch, gen, heads, sq, sk):
+    """N(0,3)/sqrt(128) scores [heads][sq][sk] with keys k > q + (sk - sq) at -inf."""
+    sc = torch.randn(heads, sq, sk, device="cuda", generator=gen) * (3.0 / 128 ** 0.5)
+    mask = torch.ones(sq, sk, dtype=torch.bool, device="cuda").triu_(1 + sk - sq)
+    return sc.masked_fill_(mask, float("-inf"))
+
+
 class BufferSet:
-    """One step's inputs and outputs."""
+    """One step's inputs and outputs (configs[4])."""
 
     def __init__(self, torch, gen):
         f = dict(device="cuda", generator=gen)
-        self.ids = torch.randint(0, VOCAB, (T,), dtype=torch.int32, **f)
-        self.emb = torch.empty(T, HIDDEN, device="cuda")
-        self.x = torch.randn(T, HIDDEN, **f)
-        self.q = torch.empty(T, HIDDEN, device="cuda")
-        self.k = torch.randn(T, NKV * HD, **f)
-        self.gate = torch.randn(T, FFN, **f)
-        self.up = torch.randn(T, FFN, **f)
-        self.act = torch.empty(T, FFN, device="cuda")
+        self.scores = causal_scores(torch, gen, SM_HEADS, SM_Q, SM_K)
+        self.gate = torch.randn(T4, FFN4, **f)
+        self.up = torch.randn(T4, FFN4, **f)
+        self.act = torch.empty(T4, FFN4, device="cuda")
+        self.q = torch.randn(T4, NQ * HD, **f)
+        self.k = torch.randn(T4, NKV * HD, **f)
 
 
 class HipEvents:
@@ -144,10 +159,9 @@ class HipEvents:
         self.made = []
 
 
-def read_traffic(kernel_key: str):
+def read_traffic(path: str = TRAFFIC_PROFILE):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary, or None if it is not there."""
-    path = os.path.join(ROOT, "profiles", f"{kernel_key}_config1_pmc.txt")
     if not os.path.exists(path):
         return None
     txt = open(path).read()
@@ -155,82 +169,118 @@ def read_traffic(kernel_key: str):
     return float(m.group(1)) if m else None
 
 
-CPU_ROWS = 64  # the CPU sample: 64 of the 512 token rows per op (same per-row shapes)
+def summarize(ts_us, nbytes, kernel):
+    """Mean and percentiles of per-launch kernel times, and GB/s of the mean."""
+    ts = sorted(ts_us)
+    mean = sum(ts) / len(ts)
+    gbps = nbytes / (mean * 1e-6) / 1e9
+    return {"us_mean": round(mean, 3), "us_p10": round(ts[len(ts) // 10], 3),
+            "us_p50": round(ts[len(ts) // 2], 3), "us_p90": round(ts[(9 * len(ts)) // 10], 3),
+            "bytes": int(nbytes), "GBps": round(gbps, 1), "frac_peak": round(gbps / PEAK_HBM_GBPS, 4),
+            "kernel": kernel, "launches": len(ts)}
 
 
-def _cpu_sample(seed: int):
-    """One thread's operands and a function running the step's three ops on
-    them through the scalar oracle (the C library; ctypes drops the GIL)."""
-    import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from oracle_py import INTERLEAVED, Oracle, make_q8_0_table as np_table
+# ---------------------------------------------------------------- CPU baseline
 
-    o = Oracle()
-    rng = np.random.default_rng(seed)
-    vocab_sample = 4096  # the gather reads random rows; a smaller table keeps setup short
-    table = np_table(rng, vocab_sample, HIDDEN)
-    ids = rng.integers(0, vocab_sample, CPU_ROWS).astype(np.int32)
-    x = rng.standard_normal((CPU_ROWS, HIDDEN)).astype(np.float32)
-    w = (1 + 0.1 * rng.standard_normal(HIDDEN)).astype(np.float32)
-    k = rng.standard_normal((CPU_ROWS, NKV, HD)).astype(np.float32)
-    g = rng.standard_normal((CPU_ROWS, FFN)).astype(np.float32)
-    u = rng.standard_normal((CPU_ROWS, FFN)).astype(np.float32)
-
-    def step():
-        o.embed_q8_0_gather(table, vocab_sample, ids, HIDDEN)
-        o.rms_norm_rope(x, w, k, NQ, HD, EPS, None, 0, THETA, INTERLEAVED)
-        o.silu_mul(g, u)
-    return step
+CPU_SAMPLE_DEN = 8  # one thread's sample: 1/8 of every op of the step (same per-row shapes)
 
 
-def _cpu_model() -> str:
-    """The host CPU's model name from /proc/cpuinfo ("unknown" elsewhere)."""
+def _cpu_model() -> dict:
+    """The host CPU as /proc/cpuinfo names it, and the logical CPUs this process may use."""
+    info = {"model_name": "unknown"}
+    keys = {"model name": "model_name", "vendor_id": "vendor", "cpu family": "family", "model": "model",
+            "stepping": "stepping", "cpu MHz": "mhz"}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k in keys:
+                    info[keys[k]] = v.strip()
     except OSError:
         pass
-    return "unknown"
+    try:
+        info["logical_cpus_usable"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["logical_cpus_usable"] = os.cpu_count()
+    return info
+
+
+def _cpu_stage_sample(den: int, seed: int):
+    """numpy operands for 1/den of the configs[4] step (SM_HEADS/den heads of
+    the causal softmax, T4/den rows of swiglu, T4/den tokens of RoPE spread
+    over positions 0..8191), and a function running `reps` passes of the
+    oracle's three ops on them, timed in C (fo_time_elementwise_stage);
+    returns the seconds per op."""
+    import ctypes
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_py import INTERLEAVED, Oracle
+
+    fn = Oracle().lib.fo_time_elementwise_stage
+    rng = np.random.default_rng(seed)
+    heads, rows = SM_HEADS // den, T4 // den
+    s = (rng.standard_normal((heads, SM_Q, SM_K), dtype=np.float32) * np.float32(3.0 / 128 ** 0.5))
+    s[:, np.triu(np.ones((SM_Q, SM_K), bool), 1)] = -np.inf
+    g = rng.standard_normal((rows, FFN4), dtype=np.float32)
+    u = rng.standard_normal((rows, FFN4), dtype=np.float32)
+    a = np.empty_like(g)
+    q = rng.standard_normal((rows, NQ, HD), dtype=np.float32)
+    k = rng.standard_normal((rows, NKV, HD), dtype=np.float32)
+    pos = (np.arange(rows) * den).astype(np.int32)
+    secs = (ctypes.c_double * 3)()
+    keep = (s, g, u, a, q, k, pos)
+
+    def run(reps):
+        fn(secs, reps, s.ctypes.data, heads, SM_Q, SM_K, a.ctypes.data, g.ctypes.data, u.ctypes.data,
+           a.size, q.ctypes.data, k.ctypes.data, rows, NQ, NKV, HD, pos.ctypes.data, THETA4, INTERLEAVED)
+        _ = keep
+        return list(secs)
+    return run
 
 
 def cpu_baseline(seconds: float):
-    """Scalar oracle on one host core over a bounded sample of the step."""
-    step = _cpu_sample(1)
-    sample_bytes = STEP_BYTES * CPU_ROWS / T
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        step()
+    """The scalar C oracle on one host core over 1/8 of the configs[4] step,
+    repeated for about `seconds` of CPU time, timed in C around each oracle
+    call (no copies, no Python in the interval)."""
+    run = _cpu_stage_sample(CPU_SAMPLE_DEN, 1)
+    tot, reps = [0.0, 0.0, 0.0], 0
+    while sum(tot) < seconds:
+        tot = [a + b for a, b in zip(tot, run(1))]
         reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(sample_bytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port", "cpu": _cpu_model(),
-            "sample": f"configs[1] step ops on {CPU_ROWS} of {T} token rows (same per-row shapes), "
-                      f"{reps} reps in {el:.1f} s, oracle incl. numpy wrapper copies"}
+    ops = list(BYTES)
+    per_op = {op: {"GBps": round(BYTES[op] / CPU_SAMPLE_DEN * reps / tot[i] / 1e9, 4),
+                   "s_per_rep": round(tot[i] / reps, 4)} for i, op in enumerate(ops)}
+    return {"value": round(STEP_BYTES / CPU_SAMPLE_DEN * reps / sum(tot) / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port", "cpu": _cpu_model(), "ops": per_op,
+            "sample": f"configs[4] step on 1/{CPU_SAMPLE_DEN} of each op (causal softmax {SM_HEADS // CPU_SAMPLE_DEN} "
+                      f"of {SM_HEADS} heads, swiglu {T4 // CPU_SAMPLE_DEN} of {T4} rows, RoPE {T4 // CPU_SAMPLE_DEN} "
+                      f"of {T4} tokens at positions 0, {CPU_SAMPLE_DEN}, ..; same per-row shapes), {reps} reps, "
+                      f"{sum(tot):.1f} s, scalar C oracle (gcc -O2, no fast-math) timed in C"}
 
 
 def cpu_baseline_all_cores(seconds: float):
     """The same oracle over rows on the host's cores: one thread per core of
-    the GPU box's share (at most 16), each running the step's ops on its own
-    64-row sample; value = all threads' bytes / wall time."""
+    the GPU box's share (at most 16), each timing its own 1/32 sample of the
+    step in C; value = all threads' bytes / wall time."""
     import threading
 
-    n = max(1, min(16, os.cpu_count() or 1))
-    steps = [_cpu_sample(1 + i) for i in range(n)]
+    n = max(1, min(16, _cpu_model()["logical_cpus_usable"] or 1))
+    den = 4 * CPU_SAMPLE_DEN
+    runs = [_cpu_stage_sample(den, 1 + i) for i in range(n)]
     counts = [0] * n
     start = threading.Barrier(n + 1)
     t_end = [0.0]
 
-    def run(i):
+    def work(i):
         start.wait()
         while time.perf_counter() < t_end[0]:
-            steps[i]()
+            runs[i](1)
             counts[i] += 1
 
-    threads = [threading.Thread(target=run, args=(i,)) for i in range(n)]
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(n)]
     for th in threads:
         th.start()
     t0 = time.perf_counter()
@@ -239,12 +289,13 @@ def cpu_baseline_all_cores(seconds: float):
     for th in threads:
         th.join()
     el = time.perf_counter() - t0
-    sample_bytes = STEP_BYTES * CPU_ROWS / T
-    return {"value": round(sample_bytes * sum(counts) / el / 1e9, 4), "unit": "GB/s", "cores": n,
-            "kind": "port", "cpu": _cpu_model(),
-            "sample": f"{n} threads, each the configs[1] step ops on its own {CPU_ROWS} token rows, "
-                      f"{sum(counts)} reps in {el:.1f} s"}
+    return {"value": round(STEP_BYTES / den * sum(counts) / el / 1e9, 4), "unit": "GB/s", "cores": n,
+            "kind": "port", "cpu": _cpu_model()["model_name"],
+            "sample": f"{n} threads, each the configs[4] step on its own 1/{den} of each op, "
+                      f"{sum(counts)} reps in {el:.1f} s wall, scalar C oracle"}
 
+
+# ---------------------------------------------------------------- GPU
 
 def main():
     args = parse()
@@ -260,22 +311,20 @@ def main():
     torch.cuda.set_device(0)
     F.lib()
     gen = torch.Generator(device="cuda").manual_seed(1234)
-    table = make_q8_0_table(torch, gen, VOCAB, HIDDEN)
-    w = 1 + 0.1 * torch.randn(HIDDEN, device="cuda", generator=gen)
-    set_bytes = sum(t.numel() * t.element_size() for t in vars(BufferSet(torch, gen)).values())
+    probe = BufferSet(torch, gen)
+    set_bytes = sum(t.numel() * t.element_size() for t in vars(probe).values())
     nsets = 1 if args.warm else max(2, -(-(1 << 30) // set_bytes) + 1)
-    sets = [BufferSet(torch, gen) for _ in range(nsets)]
+    sets = [probe] + [BufferSet(torch, gen) for _ in range(nsets - 1)]
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
 
     def launch(op, b):
-        if op == "gather":
-            F.embed_q8_0_gather(b.emb.data_ptr(), table.data_ptr(), VOCAB, b.ids.data_ptr(), T, HIDDEN, sh)
-        elif op == "norm_rope":
-            F.rms_norm_rope(b.q.data_ptr(), b.x.data_ptr(), w.data_ptr(), b.k.data_ptr(), T, NQ, NKV, HD,
-                            EPS, None, 0, THETA, F.ROPE_INTERLEAVED, sh)
+        if op == "softmax":
+            F.softmax_causal(b.scores.data_ptr(), SM_HEADS, SM_Q, SM_K, sh)
+        elif op == "swiglu":
+            F.swiglu(b.act.data_ptr(), b.gate.data_ptr(), b.up.data_ptr(), T4 * FFN4, sh)
         else:
-            F.swiglu(b.act.data_ptr(), b.gate.data_ptr(), b.up.data_ptr(), T * FFN, sh)
+            F.rope(b.q.data_ptr(), b.k.data_ptr(), T4, NQ, NKV, HD, None, 0, THETA4, F.ROPE_INTERLEAVED, sh)
 
     ops = list(BYTES)
     for i in range(args.warmup):
@@ -284,9 +333,8 @@ def main():
 
     # Timed region: K steps of plain launches.  Any per-launch timing event
     # inside it perturbs the step (a hooked launch costs ~10 us of host time
-    # and keeps the next kernel from starting under the previous one's tail;
-    # measured: 34 us per step hooked vs 25 us plain), so kernel durations
-    # come from the passes after it.
+    # and keeps the next kernel from starting under the previous one's tail),
+    # so kernel durations come from the passes after it.
     hev = HipEvents()
     torch.cuda.synchronize()
     t_start = torch.cuda.Event(enable_timing=True)
@@ -303,58 +351,52 @@ def main():
     ms_total = t_start.elapsed_time(t_end)
     ms_per_step = ms_total / args.steps
 
-    def summarize(op, ts_us):
-        ts = sorted(ts_us)
-        mean = sum(ts) / len(ts)
-        return {
-            "us_mean": round(mean, 3),
-            "us_p10": round(ts[len(ts) // 10], 3),
-            "us_p50": round(ts[len(ts) // 2], 3),
-            "us_p90": round(ts[(9 * len(ts)) // 10], 3),
-            "bytes": BYTES[op],
-            "GBps": round(BYTES[op] / (mean * 1e-6) / 1e9, 1),
-            "frac_peak": round(BYTES[op] / (mean * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
-            "kernel": KERNEL_NAMES[op],
-            "launches": len(ts),
-        }
-
     # Kernel passes: each op launched alone, every launch recording its own
     # kernel start/end (hipExtLaunchKernel events on the launch stream), over
     # the same cold rotation of buffer sets.  The dominant kernel gets K
     # launches -- as many as the timed region ran -- the others fewer.
     per_op = {}
     for op in [DOMINANT] + [o for o in ops if o != DOMINANT]:
-        reps = args.steps if op == DOMINANT else max(20, min(args.steps, 200))
+        reps = args.steps if op == DOMINANT else max(20, min(args.steps, 100))
         evs = [(hev.create(), hev.create()) for _ in range(reps)]
         for i in range(reps):
             F.time_next_launch(*evs[i])
             launch(op, sets[i % nsets])
         torch.cuda.synchronize()
-        per_op[op] = summarize(op, [hev.elapsed_ms(a, b) * 1e3 for a, b in evs])
+        per_op[op] = summarize([hev.elapsed_ms(a, b) * 1e3 for a, b in evs], BYTES[op], KERNEL_NAMES[op])
     per_op = {op: per_op[op] for op in ops}
+    per_op["softmax"]["generic_bytes"] = SOFTMAX_GENERIC_BYTES
     hev.destroy_all()
     dom = per_op[DOMINANT]
+    del sets, probe
+    torch.cuda.empty_cache()
 
     value = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
-    traffic = read_traffic(DOMINANT)
+    traffic = read_traffic()
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                 "frac": dom["frac_peak"], "traffic": traffic, "kernel": KERNEL_NAMES[DOMINANT],
                 "algorithmic_bytes_per_launch": BYTES[DOMINANT], "us_mean": dom["us_mean"],
                 "us_p50": dom["us_p50"], "launches_timed": dom["launches"],
                 "timing": "kernel start/end events of each launch (hipExtLaunchKernel), dominant-kernel "
-                          "pass after the timed region, same cold buffer rotation"}
+                          "pass after the timed region, same cold buffer rotation",
+                "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT)}
 
+    configs = {}
+    if args.config_reps > 0:
+        for r in measure_configs(torch, F, args.config_reps, extended=False):
+            configs.setdefault(str(r.pop("config")), {})[r.pop("key")] = r
     decode = decode_op_set(torch, F, gen, args.decode_reps)
     lm_head = lm_head_gemv(torch, F, gen, args.lm_head_reps)
-    del sets
-    torch.cuda.empty_cache()
     decode_model = decode_qwen3_4b(torch, args.decode_tokens)
     copy_gbps = copy_calibration(torch)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     cpu_all = None if args.no_cpu else cpu_baseline_all_cores(args.cpu_seconds / 2)
     if args.all:
-        all_configs(torch, F, args.all, args.all_reps)
+        res = measure_configs(torch, F, args.all_reps, extended=True)
+        with open(args.all, "w") as fh:
+            json.dump({"peak_GBps": PEAK_HBM_GBPS, "reps": args.all_reps,
+                       "timing": "kernel start/end events (hipExtLaunchKernel)", "results": res}, fh, indent=1)
 
     line = {
         "metric": METRIC,
@@ -368,17 +410,18 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded torch generator on device; Q8_0 scales |N(0,0.02)|/127 as fp16, "
-                "int8 uniform [-127,127])",
-        "config": {"workload": "configs[1] Llama-3-8B prefill T=512: q8_0 gather 512x4096 (vocab 128256) "
-                               "+ rms_norm->interleaved RoPE on Q[512x32x128] with RoPE on K[512x8x128] "
-                               "+ swiglu [512x14336]",
-                   "tokens": T, "hidden": HIDDEN, "heads": [NQ, NKV, HD], "ffn": FFN, "vocab": VOCAB,
+        "data": "synthetic (seeded torch generator on device: scores N(0,3)/sqrt(128) with k > q at -inf, "
+                "gate/up/q/k N(0,1); Q8_0 scales |N(0,0.02)|/127 as fp16, int8 uniform [-127,127])",
+        "config": {"workload": "configs[4] Mixtral-8x7B elementwise stage: causal softmax 32x2048x2048 "
+                               "(masked keys skipped) + swiglu [8192x14336] + interleaved RoPE "
+                               "(theta 1e6) on Q[8192x32x128] and K[8192x8x128]",
+                   "softmax": [SM_HEADS, SM_Q, SM_K], "tokens": T4, "ffn": FFN4, "heads": [NQ, NKV, HD],
                    "cache": "warm" if args.warm else f"cold ({nsets} rotating buffer sets)",
                    "step_bytes": STEP_BYTES},
         "frac_peak": round(value / PEAK_HBM_GBPS, 4),
         "ops": per_op,
         "roofline": roofline,
+        "configs": configs,
         "decode_op_set_llama3_8b": decode,
         "lm_head_gemv_q8_0": lm_head,
         "decode_qwen3_4b": decode_model,
@@ -388,6 +431,234 @@ def main():
         "wall_s_timed": round(wall, 4),
     }
     print(json.dumps(line), flush=True)
+
+
+def measure_configs(torch, F, reps, extended):
+    """Every hot-path op of BASELINE.json configs[0..3] (and, with `extended`,
+    the decode-path ops of configs[0..1] and configs[4]'s other forms) on
+    seeded synthetic inputs.  Each launch records its own kernel start/end;
+    inputs rotate over enough buffer sets (>= 1 GiB in total, at least 2)
+    that no launch finds its data in the Infinity Cache or the L2s, and
+    inputs under 16 MB are evicted by an untimed 1 GiB write before each
+    launch.  Bytes are algorithmic (inputs read once, outputs written once).
+    Returns a list of per-op records, each with its config and key."""
+    gen = torch.Generator(device="cuda").manual_seed(99)
+    dev = dict(device="cuda")
+    hev = HipEvents()
+    sh = torch.cuda.current_stream().cuda_stream
+    results = []
+
+    def nsets_for(set_bytes):
+        return max(2, -(-(1 << 30) // max(set_bytes, 1)) + 1)
+
+    scrub = {"buf": None}
+
+    def measure(cfg, key, name, nbytes, make_set, run, kernel, note="", launches=1):
+        """launches: kernels the call runs; the timing spans the first one's
+        start to the last one's end."""
+        probe = make_set()
+        sb = sum(t.numel() * t.element_size() for t in probe.values() if torch.is_tensor(t))
+        small = sb < (16 << 20)
+        sets = [probe] + [make_set() for _ in range(1 if small else nsets_for(sb) - 1)]
+        if small and scrub["buf"] is None:
+            scrub["buf"] = torch.empty((1 << 30) // 4, **dev)
+        for i in range(3):
+            run(sets[i % len(sets)])
+        evs = [(hev.create(), hev.create()) for _ in range(reps)]
+        for i in range(reps):
+            if small:  # untimed 1 GiB write evicts the small inputs from every cache level
+                scrub["buf"].zero_()
+            F.time_next_launches(*evs[i], launches)
+            run(sets[i % len(sets)])
+        torch.cuda.synchronize()
+        r = summarize([hev.elapsed_ms(a, b) * 1e3 for a, b in evs], nbytes, kernel)
+        hev.destroy_all()
+        r = {"config": cfg, "key": key, "op": name, **r, "launches_per_call": launches, "sets": len(sets),
+             "cold": "1 GiB scrub between launches" if small else "rotating buffer sets"}
+        if note:
+            r["note"] = note
+        results.append(r)
+        print(f"[cfg{cfg}] {name:40s} {r['us_mean']:9.2f} us  {r['GBps']:8.1f} GB/s  "
+              f"{100 * r['frac_peak']:5.1f}%  ({nbytes / 1e6:.2f} MB, {len(sets)} sets)", file=sys.stderr, flush=True)
+        del sets, probe
+        torch.cuda.empty_cache()
+
+    def randn(*shape):
+        return torch.randn(*shape, **dev, generator=gen)
+
+    h16 = dict(dtype=torch.int16, device="cuda")
+
+    # ---- configs[0]: Qwen3-4B decode, one token, fp32
+    E0, F0, V0 = 2560, 9728, 151936
+    pos0 = int(torch.randint(0, 4096, (1,), generator=torch.Generator().manual_seed(0)).item())
+    measure(0, "rms_norm", "rms_norm 2560", 3 * E0 * 4,
+            lambda: dict(x=randn(E0), w=1 + 0.1 * randn(E0), o=torch.empty(E0, **dev)),
+            lambda b: F.rms_norm(b["o"].data_ptr(), b["x"].data_ptr(), b["w"].data_ptr(), E0, 1e-6, sh),
+            "rms_rows_vec_kernel")
+    measure(0, "qk_norm_rope", "qk_norm_rope neox 32+8x128", 2 * 40 * 128 * 4 + 2 * 128 * 4,
+            lambda: dict(q=randn(32 * 128), k=randn(8 * 128), wq=1 + 0.1 * randn(128), wk=1 + 0.1 * randn(128)),
+            lambda b: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), b["wq"].data_ptr(), b["wk"].data_ptr(),
+                                     1, 32, 8, 128, 1e-6, None, pos0, 1e6, F.ROPE_NEOX, sh),
+            "head_ops_vec_kernel", note=f"position {pos0}")
+    measure(0, "swiglu", "swiglu 9728", 3 * F0 * 4,
+            lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), F0, sh),
+            "swiglu_vec_kernel")
+    tab0 = [make_q8_0_table(torch, gen, V0, E0) for _ in range(2)]
+    tok0 = int(torch.randint(0, V0, (1,), generator=torch.Generator().manual_seed(1)).item())
+    flip = {"i": 0}
+
+    def embed0(b):
+        flip["i"] ^= 1
+        F.embed_q8_0(b["o"].data_ptr(), tab0[flip["i"]].data_ptr(), tok0, E0, sh)
+    measure(0, "embed_q8_0", "embed_q8_0 1 id x 2560", E0 * 4 + E0 // 32 * 34 + 4,
+            lambda: dict(o=torch.empty(E0, **dev)), embed0, "q8_gather_kernel")
+    del tab0
+    if extended:
+        # layer-boundary epilogue (qwen3.cu:310-325): fused, and the reference's separate passes
+        measure(0, "residual_rms_norm_f16", "residual->rms_norm->f16 2560 (fused)", E0 * (4 + 4 + 4 + 2 + 4),
+                lambda: dict(h=randn(E0), r=randn(E0), w=1 + 0.1 * randn(E0), o=torch.empty(E0, **h16)),
+                lambda b: F.residual_rms_norm_f16(b["h"].data_ptr(), b["r"].data_ptr(), b["w"].data_ptr(), None,
+                                                  b["o"].data_ptr(), 1, E0, 1e-6, sh), "rms_rows_vec_kernel")
+        measure(0, "residual_add", "residual_add 2560 (unfused part)", 3 * E0 * 4,
+                lambda: dict(h=randn(E0), r=randn(E0)),
+                lambda b: F.residual_add(b["h"].data_ptr(), b["r"].data_ptr(), E0, sh), "convert_vec_kernel")
+        measure(0, "f32_to_f16", "f32_to_f16 2560 (unfused part)", E0 * 6,
+                lambda: dict(x=randn(E0), o=torch.empty(E0, **h16)),
+                lambda b: F.f32_to_f16(b["o"].data_ptr(), b["x"].data_ptr(), E0, sh), "convert_vec_kernel")
+        measure(0, "swiglu_f16", "swiglu->f16 9728 (fused)", F0 * 10,
+                lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **h16)),
+                lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), F0, sh),
+                "swiglu_vec_kernel")
+        # Q6_K projections of one Qwen3-4B decode layer (qwen3.cu:281-337), x in binary16
+        for pname, (pm, pk) in (("q", (4096, 2560)), ("k/v", (1024, 2560)), ("o", (2560, 4096)),
+                                ("gate/up", (9728, 2560)), ("down", (2560, 9728))):
+            measure(0, f"gemv_q6k_{pname}", f"gemv_q6k {pname} {pm}x{pk}", q6k_bytes(pm, pk),
+                    lambda pm=pm, pk=pk: dict(W=make_q6k_table(torch, gen, pm, pk), x=randn(pk).half(),
+                                              y=torch.empty(pm, **dev)),
+                    lambda b, pm=pm, pk=pk: F.gemv_q6k(b["W"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(),
+                                                       pm, pk, sh), "gemv_q6k_staged_kernel")
+        # decode attention over the binary16 KV cache (qwen3.cu:302-305), Qwen3-4B heads, max_ctx 4096
+        for seqa in (256, 1024, 2915, 4096):
+            measure(0, f"gqa_attention_{seqa}", f"gqa_attention 32q/8kv x128 seq {seqa} (+merge)",
+                    seqa * 1024 * 2 * 2 + 4096 * 8,
+                    lambda: dict(kc=randn(4096, 1024).half(), vc=randn(4096, 1024).half(), q=randn(4096) * 0.3,
+                                 o=torch.empty(4096, **dev), ws=torch.empty(32 * 4096, **dev)),
+                    lambda b, seqa=seqa: F.gqa_attention(b["o"].data_ptr(), b["q"].data_ptr(), b["kc"].data_ptr(),
+                                                         b["vc"].data_ptr(), 128, 32, 8, seqa, 4096,
+                                                         b["ws"].data_ptr(), sh),
+                    "attn_split_kernel", launches=1 if seqa <= 64 else 2)
+        measure(0, "store_kv", "store_kv 8x128 (one position)", 1024 * (4 + 2) * 2,
+                lambda: dict(kc=torch.empty(4096, 1024, dtype=torch.float16, device="cuda"),
+                             vc=torch.empty(4096, 1024, dtype=torch.float16, device="cuda"),
+                             k=randn(1024), v=randn(1024)),
+                lambda b: F.store_kv(b["kc"].data_ptr(), b["vc"].data_ptr(), b["k"].data_ptr(), b["v"].data_ptr(),
+                                     2915, 1024, 4096, sh), "store_kv_kernel")
+        measure(0, "argmax", f"argmax {V0} (one workgroup)", V0 * 4 + 4,
+                lambda: dict(x=randn(V0), r=torch.empty(1, dtype=torch.int32, device="cuda")),
+                lambda b: F.argmax(b["x"].data_ptr(), b["r"].data_ptr(), V0, sh), "argmax_kernel")
+        measure(0, "argmax_ws", f"argmax {V0} (many workgroups + merge)", V0 * 4 + 4,
+                lambda: dict(x=randn(V0), r=torch.empty(1, dtype=torch.int32, device="cuda"),
+                             ws=torch.empty(1024, dtype=torch.int64, device="cuda")),
+                lambda b: F.argmax_ws(b["x"].data_ptr(), b["r"].data_ptr(), V0, b["ws"].data_ptr(), 8192, sh),
+                "argmax_kernel", launches=2)
+        # tied LM head (qwen3.cu:261): the whole table is read once per decoded token
+        measure(0, "gemv_q8_0", f"gemv_q8_0 lm head {V0}x{E0}", gemv_bytes(V0, E0),
+                lambda: dict(t=make_q8_0_table(torch, gen, V0, E0), x=randn(E0), y=torch.empty(V0, **dev)),
+                lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V0, E0, sh),
+                "gemv_q8_0_staged_kernel")
+
+    # ---- configs[1]: Llama-3-8B prefill T=512
+    T1, H1, F1, V1 = 512, L3_HIDDEN, L3_FFN, L3_VOCAB
+    w1 = 1 + 0.1 * randn(H1)
+    tab1 = make_q8_0_table(torch, gen, V1, H1)
+    measure(1, "gather", "q8_0 gather 512 x 4096", T1 * H1 * 4 + T1 * (H1 // 32 * 34) + T1 * 4,
+            lambda: dict(ids=torch.randint(0, V1, (T1,), dtype=torch.int32, **dev, generator=gen),
+                         o=torch.empty(T1, H1, **dev)),
+            lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), T1, H1, sh),
+            "q8_gather_kernel")
+    del tab1
+    measure(1, "norm_rope", "rms_norm->rope interleaved Q+K", 2 * T1 * H1 * 4 + H1 * 4 + 2 * T1 * NKV * HD * 4,
+            lambda: dict(x=randn(T1, H1), o=torch.empty(T1, H1, **dev), k=randn(T1, NKV * HD)),
+            lambda b: F.rms_norm_rope(b["o"].data_ptr(), b["x"].data_ptr(), w1.data_ptr(), b["k"].data_ptr(),
+                                      T1, NQ, NKV, HD, 1e-5, None, 0, L3_THETA, F.ROPE_INTERLEAVED, sh),
+            "head_ops_vec_kernel")
+    measure(1, "swiglu", "swiglu 512x14336", 3 * T1 * F1 * 4,
+            lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh),
+            "swiglu_vec_kernel")
+    if extended:
+        measure(1, "residual_rms_norm_f16", "residual->rms_norm->f16 512x4096", T1 * H1 * (4 + 4 + 4 + 2) + 4 * H1,
+                lambda: dict(h=randn(T1, H1), r=randn(T1, H1), o=torch.empty(T1, H1, **h16)),
+                lambda b: F.residual_rms_norm_f16(b["h"].data_ptr(), b["r"].data_ptr(), w1.data_ptr(), None,
+                                                  b["o"].data_ptr(), T1, H1, 1e-5, sh), "rms_rows_vec_kernel")
+        measure(1, "swiglu_f16", "swiglu->f16 512x14336", T1 * F1 * (4 + 4 + 2),
+                lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **h16)),
+                lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh),
+                "swiglu_vec_kernel")
+        for pname, (pm, pk) in (("q", (4096, 4096)), ("gate/up", (14336, 4096)), ("down", (4096, 14336))):
+            measure(1, f"gemv_q6k_{pname}", f"gemv_q6k {pname} {pm}x{pk}", q6k_bytes(pm, pk),
+                    lambda pm=pm, pk=pk: dict(W=make_q6k_table(torch, gen, pm, pk), x=randn(pk).half(),
+                                              y=torch.empty(pm, **dev)),
+                    lambda b, pm=pm, pk=pk: F.gemv_q6k(b["W"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(),
+                                                       pm, pk, sh), "gemv_q6k_staged_kernel")
+        measure(1, "gemv_q8_0", f"gemv_q8_0 lm head {V1}x{H1}", gemv_bytes(V1, H1),
+                lambda: dict(t=make_q8_0_table(torch, gen, V1, H1), x=randn(H1), y=torch.empty(V1, **dev)),
+                lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V1, H1, sh),
+                "gemv_q8_0_staged_kernel")
+
+    # ---- configs[2]: Qwen3-8B long prefill T=4096
+    T2, F2 = 4096, 12288
+    wq2, wk2 = 1 + 0.1 * randn(HD), 1 + 0.1 * randn(HD)
+    styles = ((F.ROPE_NEOX, "neox"),) + (((F.ROPE_INTERLEAVED, "interleaved"),) if extended else ())
+    for style, sname in styles:
+        measure(2, "qk_norm_rope" if sname == "neox" else f"qk_norm_rope_{sname}",
+                f"qk_norm_rope {sname} 4096x(32+8)x128", 2 * T2 * (NQ + NKV) * HD * 4 + 2 * HD * 4,
+                lambda: dict(q=randn(T2, NQ * HD), k=randn(T2, NKV * HD)),
+                lambda b, style=style: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), wq2.data_ptr(),
+                                                      wk2.data_ptr(), T2, NQ, NKV, HD, 1e-6, None, 0, 1e6,
+                                                      style, sh), "head_ops_vec_kernel")
+    measure(2, "swiglu", "swiglu 4096x12288", 3 * T2 * F2 * 4,
+            lambda: dict(g=randn(T2, F2), u=randn(T2, F2), o=torch.empty(T2, F2, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T2 * F2, sh),
+            "swiglu_vec_kernel")
+
+    # ---- configs[3]: Qwen3-14B embedding batch, gather -> rms_norm, Zipf ids
+    T3, E3, V3 = 8192, 5120, 151936
+    w3 = 1 + 0.1 * randn(E3)
+    tabs3 = [make_q8_0_table(torch, gen, V3, E3) for _ in range(2)]
+    zw = torch.arange(1, V3 + 1, dtype=torch.float64) ** -1.1
+    zcdf = torch.cumsum(zw, 0)
+    zcdf /= zcdf[-1].clone()
+    zg = torch.Generator().manual_seed(3)
+    u3 = torch.rand(T3, generator=zg, dtype=torch.float64)
+    ids3 = torch.clamp(torch.searchsorted(zcdf, u3), max=V3 - 1).to(torch.int32).cuda()
+    uniq = int(torch.unique(ids3).numel())
+    flip3 = {"i": 0}
+
+    def gather3(b):
+        flip3["i"] ^= 1
+        F.embed_q8_0_gather_rms_norm(b["o"].data_ptr(), tabs3[flip3["i"]].data_ptr(), V3, b["ids"].data_ptr(),
+                                     T3, E3, w3.data_ptr(), 1e-6, sh)
+    measure(3, "gather_rms_norm", "gather->rms_norm 8192 Zipf x 5120",
+            T3 * E3 * 4 + uniq * (E3 // 32 * 34) + T3 * 4 + E3 * 4,
+            lambda: dict(ids=ids3, o=torch.empty(T3, E3, **dev)), gather3, "q8_gather_rms_kernel",
+            note=f"{uniq} unique rows; per-token-read bytes {T3 * E3 * 4 + T3 * (E3 // 32 * 34) + T3 * 4 + E3 * 4}")
+    del tabs3
+
+    if extended:
+        # ---- configs[4]: the step's ops in other forms
+        measure(4, "softmax_rows_generic", "softmax rows 65536x2048 (generic)", SOFTMAX_GENERIC_BYTES,
+                lambda: dict(s=causal_scores(torch, gen, SM_HEADS, SM_Q, SM_K)),
+                lambda b: F.softmax_rows(b["s"].data_ptr(), SM_HEADS * SM_Q, SM_K, SM_K, sh), "softmax_vec_kernel")
+        measure(4, "swiglu_f16", "swiglu->f16 8192x14336", T4 * FFN4 * (4 + 4 + 2),
+                lambda: dict(g=randn(T4, FFN4), u=randn(T4, FFN4), o=torch.empty(T4, FFN4, **h16)),
+                lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), T4 * FFN4, sh),
+                "swiglu_vec_kernel")
+    if scrub["buf"] is not None:
+        scrub["buf"] = None
+        torch.cuda.empty_cache()
+    return results
 
 
 def decode_qwen3_4b(torch, tokens):
@@ -464,23 +735,23 @@ def lm_head_gemv(torch, F, gen, reps):
         return None
     hev = HipEvents()
     sh = torch.cuda.current_stream().cuda_stream
-    tables = [make_q8_0_table(torch, gen, VOCAB, HIDDEN) for _ in range(3)]
-    x = torch.randn(HIDDEN, device="cuda", generator=gen)
-    y = torch.empty(VOCAB, device="cuda")
+    tables = [make_q8_0_table(torch, gen, L3_VOCAB, L3_HIDDEN) for _ in range(3)]
+    x = torch.randn(L3_HIDDEN, device="cuda", generator=gen)
+    y = torch.empty(L3_VOCAB, device="cuda")
     for i in range(3):
-        F.gemv_q8_0(tables[i].data_ptr(), x.data_ptr(), y.data_ptr(), VOCAB, HIDDEN, sh)
+        F.gemv_q8_0(tables[i].data_ptr(), x.data_ptr(), y.data_ptr(), L3_VOCAB, L3_HIDDEN, sh)
     evs = [(hev.create(), hev.create()) for _ in range(reps)]
     for i in range(reps):
         F.time_next_launch(*evs[i])
-        F.gemv_q8_0(tables[i % 3].data_ptr(), x.data_ptr(), y.data_ptr(), VOCAB, HIDDEN, sh)
+        F.gemv_q8_0(tables[i % 3].data_ptr(), x.data_ptr(), y.data_ptr(), L3_VOCAB, L3_HIDDEN, sh)
     torch.cuda.synchronize()
     ts = sorted(hev.elapsed_ms(a, b) * 1e3 for a, b in evs)
     hev.destroy_all()
     del tables
     torch.cuda.empty_cache()
     mean = sum(ts) / len(ts)
-    nbytes = gemv_bytes(VOCAB, HIDDEN)
-    return {"shape": [VOCAB, HIDDEN], "bytes": nbytes, "us_mean": round(mean, 3),
+    nbytes = gemv_bytes(L3_VOCAB, L3_HIDDEN)
+    return {"shape": [L3_VOCAB, L3_HIDDEN], "bytes": nbytes, "us_mean": round(mean, 3),
             "us_p50": round(ts[len(ts) // 2], 3), "us_p10": round(ts[len(ts) // 10], 3),
             "GBps": round(nbytes / (mean * 1e-6) / 1e9, 1),
             "frac_peak": round(nbytes / (mean * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
@@ -495,28 +766,28 @@ def decode_op_set(torch, F, gen, reps):
         return None
     max_ctx = 4096
     pos = int(torch.randint(0, max_ctx, (1,), generator=torch.Generator().manual_seed(5)).item())
-    table = make_q8_0_table(torch, gen, VOCAB, HIDDEN)
-    hidden = torch.empty(HIDDEN, device="cuda")
-    normed = torch.empty(HIDDEN, device="cuda")
-    w1 = 1 + 0.1 * torch.randn(HIDDEN, device="cuda", generator=gen)
-    w2 = 1 + 0.1 * torch.randn(HIDDEN, device="cuda", generator=gen)
+    table = make_q8_0_table(torch, gen, L3_VOCAB, L3_HIDDEN)
+    hidden = torch.empty(L3_HIDDEN, device="cuda")
+    normed = torch.empty(L3_HIDDEN, device="cuda")
+    w1 = 1 + 0.1 * torch.randn(L3_HIDDEN, device="cuda", generator=gen)
+    w2 = 1 + 0.1 * torch.randn(L3_HIDDEN, device="cuda", generator=gen)
     q = torch.randn(NQ * HD, device="cuda", generator=gen)
     k = torch.randn(NKV * HD, device="cuda", generator=gen)
     scores = torch.randn(NQ, max_ctx, device="cuda", generator=gen) * (3 / 128 ** 0.5)
-    gate = torch.randn(FFN, device="cuda", generator=gen)
-    up = torch.randn(FFN, device="cuda", generator=gen)
-    act = torch.empty(FFN, device="cuda")
+    gate = torch.randn(L3_FFN, device="cuda", generator=gen)
+    up = torch.randn(L3_FFN, device="cuda", generator=gen)
+    act = torch.empty(L3_FFN, device="cuda")
     s = torch.cuda.current_stream()
     sh = s.cuda_stream
     tok = 9707
 
     def step():
-        F.embed_q8_0(hidden.data_ptr(), table.data_ptr(), tok, HIDDEN, sh)
-        F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w1.data_ptr(), HIDDEN, 1e-5, sh)
-        F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, THETA, F.ROPE_INTERLEAVED, sh)
+        F.embed_q8_0(hidden.data_ptr(), table.data_ptr(), tok, L3_HIDDEN, sh)
+        F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w1.data_ptr(), L3_HIDDEN, 1e-5, sh)
+        F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, L3_THETA, F.ROPE_INTERLEAVED, sh)
         F.softmax_rows(scores.data_ptr(), NQ, pos + 1, max_ctx, sh)
-        F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), HIDDEN, 1e-5, sh)
-        F.silu_elementwise_mul(act.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh)
+        F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), L3_HIDDEN, 1e-5, sh)
+        F.silu_elementwise_mul(act.data_ptr(), gate.data_ptr(), up.data_ptr(), L3_FFN, sh)
 
     for _ in range(20):
         step()
@@ -553,12 +824,12 @@ def decode_op_set(torch, F, gen, reps):
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
             sh_cap = torch.cuda.current_stream().cuda_stream
-            F.embed_q8_0(hidden.data_ptr(), table.data_ptr(), tok, HIDDEN, sh_cap)
-            F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w1.data_ptr(), HIDDEN, 1e-5, sh_cap)
-            F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, THETA, F.ROPE_INTERLEAVED, sh_cap)
+            F.embed_q8_0(hidden.data_ptr(), table.data_ptr(), tok, L3_HIDDEN, sh_cap)
+            F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w1.data_ptr(), L3_HIDDEN, 1e-5, sh_cap)
+            F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, L3_THETA, F.ROPE_INTERLEAVED, sh_cap)
             F.softmax_rows(scores.data_ptr(), NQ, pos + 1, max_ctx, sh_cap)
-            F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), HIDDEN, 1e-5, sh_cap)
-            F.silu_elementwise_mul(act.data_ptr(), gate.data_ptr(), up.data_ptr(), FFN, sh_cap)
+            F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), L3_HIDDEN, 1e-5, sh_cap)
+            F.silu_elementwise_mul(act.data_ptr(), gate.data_ptr(), up.data_ptr(), L3_FFN, sh_cap)
         for _ in range(10):
             g.replay()
         torch.cuda.synchronize()
@@ -591,233 +862,6 @@ def q6k_bytes(m, k):
 def gemv_bytes(m, k):
     """Algorithmic bytes of y[m] = W x over a Q8_0 W: the table once, x, y."""
     return m * (k // 32) * 34 + 4 * k + 4 * m
-
-
-def all_configs(torch, F, path, reps):
-    """Every op of BASELINE.json configs[0..4] on seeded synthetic inputs.
-    Each launch records its own kernel start/end; inputs rotate over enough
-    buffer sets (>= 1 GiB in total, at least 2) that no launch finds its data
-    in the Infinity Cache or the L2s.  Bytes are algorithmic (inputs read
-    once, outputs written once)."""
-    gen = torch.Generator(device="cuda").manual_seed(99)
-    dev = dict(device="cuda")
-    hev = HipEvents()
-    sh = torch.cuda.current_stream().cuda_stream
-    results = []
-
-    def nsets_for(set_bytes):
-        return max(2, -(-(1 << 30) // max(set_bytes, 1)) + 1)
-
-    scrub = {"buf": None}
-
-    def measure(cfg, name, nbytes, make_set, run, note="", launches=1):
-        """launches: kernels the call runs; the timing spans the first one's
-        start to the last one's end."""
-        probe = make_set()
-        sb = sum(t.numel() * t.element_size() for t in probe.values() if torch.is_tensor(t))
-        small = sb < (16 << 20)
-        sets = [probe] + [make_set() for _ in range(1 if small else nsets_for(sb) - 1)]
-        if small and scrub["buf"] is None:
-            scrub["buf"] = torch.empty((1 << 30) // 4, **dev)
-        for i in range(3):
-            run(sets[i % len(sets)])
-        evs = [(hev.create(), hev.create()) for _ in range(reps)]
-        for i in range(reps):
-            if small:  # untimed 1 GiB write evicts the small inputs from every cache level
-                scrub["buf"].zero_()
-            F.time_next_launches(*evs[i], launches)
-            run(sets[i % len(sets)])
-        torch.cuda.synchronize()
-        ts = sorted(hev.elapsed_ms(a, b) * 1e3 for a, b in evs)
-        mean = sum(ts) / len(ts)
-        gbps = nbytes / (mean * 1e-6) / 1e9
-        r = {"config": cfg, "op": name, "bytes": int(nbytes), "us_mean": round(mean, 3),
-             "launches": launches,
-             "us_p10": round(ts[len(ts) // 10], 3), "us_p50": round(ts[len(ts) // 2], 3),
-             "us_p90": round(ts[(9 * len(ts)) // 10], 3), "GBps": round(gbps, 1),
-             "frac_peak": round(gbps / PEAK_HBM_GBPS, 4), "sets": len(sets),
-             "cold": "1 GiB scrub between launches" if small else "rotating buffer sets"}
-        if note:
-            r["note"] = note
-        results.append(r)
-        print(f"[all] cfg{cfg} {name:34s} {mean:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / PEAK_HBM_GBPS:5.1f}%"
-              f"  ({nbytes / 1e6:.2f} MB, {len(sets)} sets)", file=sys.stderr, flush=True)
-        del sets
-        torch.cuda.empty_cache()
-
-    def randn(*shape):
-        return torch.randn(*shape, **dev, generator=gen)
-
-    # ---- configs[0]: Qwen3-4B decode, one token, fp32
-    E0, F0, V0 = 2560, 9728, 151936
-    pos0 = int(torch.randint(0, 4096, (1,), generator=torch.Generator().manual_seed(0)).item())
-    measure(0, "rms_norm 2560", 3 * E0 * 4,
-            lambda: dict(x=randn(E0), w=1 + 0.1 * randn(E0), o=torch.empty(E0, **dev)),
-            lambda b: F.rms_norm(b["o"].data_ptr(), b["x"].data_ptr(), b["w"].data_ptr(), E0, 1e-6, sh))
-    measure(0, "qk_norm_rope neox 32+8x128", 2 * 40 * 128 * 4 + 2 * 128 * 4,
-            lambda: dict(q=randn(32 * 128), k=randn(8 * 128), wq=1 + 0.1 * randn(128), wk=1 + 0.1 * randn(128)),
-            lambda b: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), b["wq"].data_ptr(), b["wk"].data_ptr(),
-                                     1, 32, 8, 128, 1e-6, None, pos0, 1e6, F.ROPE_NEOX, sh))
-    measure(0, "swiglu 9728", 3 * F0 * 4,
-            lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **dev)),
-            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), F0, sh))
-    tab0 = [make_q8_0_table(torch, gen, V0, E0) for _ in range(2)]
-    tok0 = int(torch.randint(0, V0, (1,), generator=torch.Generator().manual_seed(1)).item())
-    flip = {"i": 0}
-
-    def embed0(b):
-        flip["i"] ^= 1
-        F.embed_q8_0(b["o"].data_ptr(), tab0[flip["i"]].data_ptr(), tok0, E0, sh)
-    measure(0, "embed_q8_0 1 id x 2560", E0 * 4 + E0 // 32 * 34 + 4,
-            lambda: dict(o=torch.empty(E0, **dev)), embed0)
-    del tab0
-    # layer-boundary epilogue (qwen3.cu:310-325): fused, and the reference's separate passes
-    h16 = dict(dtype=torch.int16, device="cuda")
-    measure(0, "residual->rms_norm->f16 2560 (fused)", E0 * (4 + 4 + 4 + 2 + 4),
-            lambda: dict(h=randn(E0), r=randn(E0), w=1 + 0.1 * randn(E0), o=torch.empty(E0, **h16)),
-            lambda b: F.residual_rms_norm_f16(b["h"].data_ptr(), b["r"].data_ptr(), b["w"].data_ptr(), None,
-                                              b["o"].data_ptr(), 1, E0, 1e-6, sh))
-    measure(0, "residual_add 2560 (unfused part)", 3 * E0 * 4,
-            lambda: dict(h=randn(E0), r=randn(E0)),
-            lambda b: F.residual_add(b["h"].data_ptr(), b["r"].data_ptr(), E0, sh))
-    measure(0, "f32_to_f16 2560 (unfused part)", E0 * 6,
-            lambda: dict(x=randn(E0), o=torch.empty(E0, **h16)),
-            lambda b: F.f32_to_f16(b["o"].data_ptr(), b["x"].data_ptr(), E0, sh))
-    measure(0, "swiglu->f16 9728 (fused)", F0 * 10,
-            lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **h16)),
-            lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), F0, sh))
-    # Q6_K projections of one Qwen3-4B decode layer (qwen3.cu:281-337), x in binary16
-    for pname, (pm, pk) in (("q", (4096, 2560)), ("k/v", (1024, 2560)), ("o", (2560, 4096)),
-                            ("gate/up", (9728, 2560)), ("down", (2560, 9728))):
-        measure(0, f"gemv_q6k {pname} {pm}x{pk}", q6k_bytes(pm, pk),
-                lambda pm=pm, pk=pk: dict(W=make_q6k_table(torch, gen, pm, pk), x=randn(pk).half(),
-                                          y=torch.empty(pm, **dev)),
-                lambda b, pm=pm, pk=pk: F.gemv_q6k(b["W"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(),
-                                                   pm, pk, sh))
-    # decode attention over the binary16 KV cache (qwen3.cu:302-305), Qwen3-4B heads, max_ctx 4096
-    for seqa in (256, 1024, 2915, 4096):
-        measure(0, f"gqa_attention 32q/8kv x128 seq {seqa} (+merge)", seqa * 1024 * 2 * 2 + 4096 * 8,
-                lambda: dict(kc=randn(4096, 1024).half(), vc=randn(4096, 1024).half(), q=randn(4096) * 0.3,
-                             o=torch.empty(4096, **dev), ws=torch.empty(32 * 4096, **dev)),
-                lambda b, seqa=seqa: F.gqa_attention(b["o"].data_ptr(), b["q"].data_ptr(), b["kc"].data_ptr(),
-                                                     b["vc"].data_ptr(), 128, 32, 8, seqa, 4096,
-                                                     b["ws"].data_ptr(), sh),
-                launches=1 if seqa <= 64 else 2)
-    measure(0, "store_kv 8x128 (one position)", 1024 * (4 + 2) * 2,
-            lambda: dict(kc=torch.empty(4096, 1024, dtype=torch.float16, device="cuda"),
-                         vc=torch.empty(4096, 1024, dtype=torch.float16, device="cuda"),
-                         k=randn(1024), v=randn(1024)),
-            lambda b: F.store_kv(b["kc"].data_ptr(), b["vc"].data_ptr(), b["k"].data_ptr(), b["v"].data_ptr(),
-                                 2915, 1024, 4096, sh))
-    measure(0, f"argmax {V0}", V0 * 4 + 4,
-            lambda: dict(x=randn(V0), r=torch.empty(1, dtype=torch.int32, device="cuda")),
-            lambda b: F.argmax(b["x"].data_ptr(), b["r"].data_ptr(), V0, sh))
-    # tied LM head (qwen3.cu:261): the whole table is read once per decoded token
-    measure(0, f"gemv_q8_0 lm head {V0}x{E0}", gemv_bytes(V0, E0),
-            lambda: dict(t=make_q8_0_table(torch, gen, V0, E0), x=randn(E0), y=torch.empty(V0, **dev)),
-            lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V0, E0, sh))
-
-    # ---- configs[1]: Llama-3-8B prefill T=512 (the bench step's ops)
-    T1, H1, F1, V1 = 512, 4096, 14336, 128256
-    w1 = 1 + 0.1 * randn(H1)
-    measure(1, "rms_norm->rope interleaved Q+K", BYTES["norm_rope"],
-            lambda: dict(x=randn(T1, H1), o=torch.empty(T1, H1, **dev), k=randn(T1, 8 * 128)),
-            lambda b: F.rms_norm_rope(b["o"].data_ptr(), b["x"].data_ptr(), w1.data_ptr(), b["k"].data_ptr(),
-                                      T1, 32, 8, 128, 1e-5, None, 0, 5e5, F.ROPE_INTERLEAVED, sh))
-    measure(1, "swiglu 512x14336", BYTES["swiglu"],
-            lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **dev)),
-            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh))
-    tab1 = make_q8_0_table(torch, gen, V1, H1)
-    measure(1, "q8_0 gather 512 x 4096", BYTES["gather"],
-            lambda: dict(ids=torch.randint(0, V1, (T1,), dtype=torch.int32, **dev, generator=gen),
-                         o=torch.empty(T1, H1, **dev)),
-            lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), T1, H1, sh))
-    del tab1
-    h16 = dict(dtype=torch.int16, device="cuda")
-    measure(1, "residual->rms_norm->f16 512x4096", T1 * H1 * (4 + 4 + 4 + 2) + 4 * H1,
-            lambda: dict(h=randn(T1, H1), r=randn(T1, H1), o=torch.empty(T1, H1, **h16)),
-            lambda b: F.residual_rms_norm_f16(b["h"].data_ptr(), b["r"].data_ptr(), w1.data_ptr(), None,
-                                              b["o"].data_ptr(), T1, H1, 1e-5, sh))
-    measure(1, "swiglu->f16 512x14336", T1 * F1 * (4 + 4 + 2),
-            lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **h16)),
-            lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh))
-    for pname, (pm, pk) in (("q", (4096, 4096)), ("gate/up", (14336, 4096)), ("down", (4096, 14336))):
-        measure(1, f"gemv_q6k {pname} {pm}x{pk}", q6k_bytes(pm, pk),
-                lambda pm=pm, pk=pk: dict(W=make_q6k_table(torch, gen, pm, pk), x=randn(pk).half(),
-                                          y=torch.empty(pm, **dev)),
-                lambda b, pm=pm, pk=pk: F.gemv_q6k(b["W"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(),
-                                                   pm, pk, sh))
-    measure(1, f"gemv_q8_0 lm head {V1}x{H1}", gemv_bytes(V1, H1),
-            lambda: dict(t=make_q8_0_table(torch, gen, V1, H1), x=randn(H1), y=torch.empty(V1, **dev)),
-            lambda b: F.gemv_q8_0(b["t"].data_ptr(), b["x"].data_ptr(), b["y"].data_ptr(), V1, H1, sh))
-
-    # ---- configs[2]: Qwen3-8B long prefill T=4096
-    T2, F2 = 4096, 12288
-    wq2, wk2 = 1 + 0.1 * randn(128), 1 + 0.1 * randn(128)
-    for style, sname in ((F.ROPE_NEOX, "neox"), (F.ROPE_INTERLEAVED, "interleaved")):
-        measure(2, f"qk_norm_rope {sname} 4096x(32+8)x128", 2 * T2 * 40 * 128 * 4 + 2 * 128 * 4,
-                lambda: dict(q=randn(T2, 32 * 128), k=randn(T2, 8 * 128)),
-                lambda b, style=style: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), wq2.data_ptr(),
-                                                      wk2.data_ptr(), T2, 32, 8, 128, 1e-6, None, 0, 1e6,
-                                                      style, sh))
-    measure(2, "swiglu 4096x12288", 3 * T2 * F2 * 4,
-            lambda: dict(g=randn(T2, F2), u=randn(T2, F2), o=torch.empty(T2, F2, **dev)),
-            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T2 * F2, sh))
-
-    # ---- configs[3]: Qwen3-14B embedding batch, gather -> rms_norm, Zipf ids
-    T3, E3, V3 = 8192, 5120, 151936
-    w3 = 1 + 0.1 * randn(E3)
-    tabs3 = [make_q8_0_table(torch, gen, V3, E3) for _ in range(2)]
-    zw = torch.arange(1, V3 + 1, dtype=torch.float64) ** -1.1
-    zcdf = torch.cumsum(zw, 0)
-    zcdf /= zcdf[-1].clone()
-    zg = torch.Generator().manual_seed(3)
-
-    def zipf_ids():
-        u = torch.rand(T3, generator=zg, dtype=torch.float64)
-        return torch.clamp(torch.searchsorted(zcdf, u), max=V3 - 1).to(torch.int32).cuda()
-    ids3 = zipf_ids()
-    uniq = int(torch.unique(ids3).numel())
-    flip3 = {"i": 0}
-
-    def gather3(b):
-        flip3["i"] ^= 1
-        F.embed_q8_0_gather_rms_norm(b["o"].data_ptr(), tabs3[flip3["i"]].data_ptr(), V3, b["ids"].data_ptr(),
-                                     T3, E3, w3.data_ptr(), 1e-6, sh)
-    measure(3, "gather->rms_norm 8192 Zipf x 5120", T3 * E3 * 4 + uniq * (E3 // 32 * 34) + T3 * 4 + E3 * 4,
-            lambda: dict(ids=ids3, o=torch.empty(T3, E3, **dev)), gather3,
-            note=f"{uniq} unique rows; per-token-read bytes {T3 * E3 * 4 + T3 * (E3 // 32 * 34) + T3 * 4 + E3 * 4}")
-    del tabs3
-
-    # ---- configs[4]: Mixtral-8x7B elementwise stage
-    H4, S4 = 32, 2048
-
-    def scores():
-        sc = randn(H4, S4, S4) * (3.0 / 128 ** 0.5)
-        return sc.masked_fill_(torch.ones(S4, S4, dtype=torch.bool, **dev).triu_(1), float("-inf"))
-    measure(4, "causal softmax 32x2048x2048 (skip)", 805437440,
-            lambda: dict(s=scores()),
-            lambda b: F.softmax_causal(b["s"].data_ptr(), H4, S4, S4, sh),
-            note="causal-skip bytes: masked keys not read, all keys written; generic bytes 1073741824")
-    measure(4, "softmax rows 65536x2048 (generic)", 1073741824,
-            lambda: dict(s=scores()),
-            lambda b: F.softmax_rows(b["s"].data_ptr(), H4 * S4, S4, S4, sh))
-    T4, F4 = 8192, 14336
-    measure(4, "swiglu 8192x14336", 3 * T4 * F4 * 4,
-            lambda: dict(g=randn(T4, F4), u=randn(T4, F4), o=torch.empty(T4, F4, **dev)),
-            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T4 * F4, sh))
-    measure(4, "swiglu->f16 8192x14336", T4 * F4 * (4 + 4 + 2),
-            lambda: dict(g=randn(T4, F4), u=randn(T4, F4), o=torch.empty(T4, F4, dtype=torch.int16, **dev)),
-            lambda b: F.swiglu_f16(b["o"].data_ptr(), None, b["g"].data_ptr(), b["u"].data_ptr(), T4 * F4, sh))
-    measure(4, "rope interleaved Q+K 8192x(32+8)x128", 2 * T4 * 40 * 128 * 4,
-            lambda: dict(q=randn(T4, 32 * 128), k=randn(T4, 8 * 128)),
-            lambda b: F.rope(b["q"].data_ptr(), b["k"].data_ptr(), T4, 32, 8, 128, None, 0, 1e6,
-                             F.ROPE_INTERLEAVED, sh))
-    hev.destroy_all()
-    scrub["buf"] = None
-    with open(path, "w") as fh:
-        json.dump({"peak_GBps": PEAK_HBM_GBPS, "reps": reps, "timing": "kernel start/end events (hipExtLaunchKernel)",
-                   "results": results}, fh, indent=1)
 
 
 def copy_calibration(torch):

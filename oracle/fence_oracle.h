@@ -167,6 +167,17 @@ void fo_rms_norm_rope(float* out, const float* x, const float* w, float* k,
                       int head_dim, float eps, const int32_t* positions,
                       int pos0, float freq_base, int style);
 
+/* CPU-baseline timing (fence_oracle_time.c; bench.py's cpu_baseline leg):
+ * `reps` passes of the elementwise stage of BASELINE configs[4] on caller
+ * buffers -- fo_softmax_causal over [heads][sq][sk], fo_silu_elementwise_mul
+ * over n elements into act, fo_rope_rows over `tokens` tokens at
+ * positions[t] -- with the seconds spent in each of the three accumulated
+ * into secs[0..2] (CLOCK_MONOTONIC around each call). */
+void fo_time_elementwise_stage(double secs[3], int reps, float* scores, int64_t heads, int sq,
+                               int sk, float* act, const float* gate, const float* up, int64_t n,
+                               float* q, float* k, int64_t tokens, int n_q_heads, int n_kv_heads,
+                               int head_dim, const int32_t* positions, float freq_base, int style);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,8 @@ _SIGS = {
     "fo_argmax": ((_P, _I), ctypes.c_int),
     "fo_qk_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
     "fo_rms_norm_rope": ((_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I), None),
+    "fo_time_elementwise_stage": ((_P, _I, _P, _L, _I, _I, _P, _P, _P, _L, _P, _P, _L, _I, _I, _I, _P, _F, _I),
+                                  None),
 }
 
 

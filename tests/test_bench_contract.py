@@ -21,9 +21,11 @@ def test_more_than_one_gpu_exits_with_a_message():
 
 def test_cpu_baseline_fields():
     b = bench.cpu_baseline(0.2)
-    assert set(b) >= {"value", "unit", "cores", "kind", "sample", "cpu"}
+    assert set(b) >= {"value", "unit", "cores", "kind", "sample", "cpu", "ops"}
     assert b["kind"] == "port" and b["cores"] == 1 and b["unit"] == "GB/s"
-    assert b["value"] > 0 and isinstance(b["cpu"], str) and b["cpu"]
+    assert b["value"] > 0 and b["cpu"]["model_name"]
+    assert set(b["ops"]) == set(bench.BYTES) and all(v["GBps"] > 0 for v in b["ops"].values())
+    assert "timed in C" in b["sample"] and "numpy" not in b["sample"]
 
 
 def test_cpu_baseline_all_cores_bounded():
@@ -31,16 +33,23 @@ def test_cpu_baseline_all_cores_bounded():
     assert 1 <= b["cores"] <= 16 and b["value"] > 0 and b["kind"] == "port"
 
 
+def test_cpu_sample_is_an_eighth_of_each_op():
+    # the sample sizes the value is scaled by: heads, rows and tokens divide evenly
+    den = bench.CPU_SAMPLE_DEN
+    assert bench.SM_HEADS % den == 0 and bench.T4 % den == 0
+
+
 def test_traffic_from_committed_profile():
-    t = bench.read_traffic(bench.DOMINANT)
-    assert t is not None, "profiles/swiglu_config1_pmc.txt missing or without traffic_bytes_per_launch"
+    t = bench.read_traffic()
+    assert t is not None, "profiles/swiglu_config4_pmc.txt missing or without traffic_bytes_per_launch"
     alg = bench.BYTES[bench.DOMINANT]
     assert abs(t / alg - 1) < 0.02, (t, alg)
 
 
-def test_step_bytes_are_the_configs1_shapes():
-    # gather: out 512 x 4096 fp32 + 512 Q8_0 rows of 4096 (128 blocks x 34 B) + 512 int32 ids
-    assert bench.BYTES["gather"] == 512 * 4096 * 4 + 512 * 128 * 34 + 512 * 4
-    # norm -> RoPE: x in + q out (512 x 4096 fp32), w, K in + out (512 x 1024)
-    assert bench.BYTES["norm_rope"] == 2 * 512 * 4096 * 4 + 4096 * 4 + 2 * 512 * 1024 * 4
-    assert bench.BYTES["swiglu"] == 3 * 512 * 14336 * 4
+def test_step_bytes_are_the_configs4_shapes():
+    # causal softmax: read keys 0..q of every query row, write all 2048 keys, 32 heads
+    assert bench.BYTES["softmax"] == 32 * (2048 * 2049 // 2) * 4 + 32 * 2048 * 2048 * 4 == 805437440
+    assert bench.BYTES["swiglu"] == 3 * 8192 * 14336 * 4 == 1409286144
+    # interleaved RoPE in place on Q [8192 x 32 x 128] and K [8192 x 8 x 128]
+    assert bench.BYTES["rope"] == 2 * 8192 * 40 * 128 * 4 == 335544320
+    assert bench.STEP_BYTES == 805437440 + 1409286144 + 335544320

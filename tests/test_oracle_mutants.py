@@ -65,7 +65,8 @@ def test_mutant_is_caught(tmp_path, mid, old, new):
     mpath.write_text(src.replace(old, new))
     so = tmp_path / f"lib_{mid}.so"
     subprocess.run(["gcc", "-std=c11", "-O2", "-fPIC", "-shared", "-ffp-contract=off",
-                    "-I", os.path.join(ROOT, "oracle"), str(mpath), "-o", str(so), "-lm"],
+                    "-I", os.path.join(ROOT, "oracle"), str(mpath), os.path.join(ROOT, "oracle", "fence_oracle_time.c"),
+                    "-o", str(so), "-lm"],
                    check=True)
     results = oracle_checks.run_all(Oracle(str(so)))
     caught = {k: v for k, v in results.items() if v}
