@@ -1,5 +1,5 @@
 // attention.hip -- decode-step attention over the binary16 KV cache, and the
-// KV store and greedy argmax, on gfx950.
+// KV store, on gfx950.
 //
 // Follows gqa_attention, src/kernels/ops.cuh:320-413: for query head h (kv
 // head h / (n_q/n_kv)), over the seq_len cached positions t,
@@ -484,59 +484,6 @@ __global__ __launch_bounds__(256) void store_kv_kernel(uint16_t* __restrict__ kc
     }
 }
 
-// argmax (greedy sampling): one workgroup of 1024 threads, float4 loads when
-// aligned; each thread keeps the first index of its largest value, and the
-// tree keeps the larger value, or the lower index on a tie.
-__global__ __launch_bounds__(1024) void argmax_kernel(int* __restrict__ result, const float* __restrict__ x, int n,
-                                                      int vec) {
-    __shared__ float bv[1024];
-    __shared__ int bi[1024];
-    float best = -1e30f;
-    int idx = 0;
-    if (vec) {
-        const int n4 = n >> 2;
-        constexpr int kBatch = 8;  // float4 loads a thread has in flight
-        for (int i0 = threadIdx.x; i0 < n4; i0 += 1024 * kBatch) {
-            f4 v[kBatch];
-#pragma unroll
-            for (int b = 0; b < kBatch; ++b) {
-                const int i = i0 + 1024 * b;
-                v[b] = ld4<true>(x + 4 * (i < n4 ? i : i0));  // clamped: inside x
-            }
-#pragma unroll
-            for (int b = 0; b < kBatch; ++b) {  // in index order, so a tie keeps the first
-                const int i = i0 + 1024 * b;
-                if (i < n4) {
-                    if (v[b].x > best) best = v[b].x, idx = 4 * i;
-                    if (v[b].y > best) best = v[b].y, idx = 4 * i + 1;
-                    if (v[b].z > best) best = v[b].z, idx = 4 * i + 2;
-                    if (v[b].w > best) best = v[b].w, idx = 4 * i + 3;
-                }
-            }
-        }
-        for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024)
-            if (x[i] > best) best = x[i], idx = i;
-    } else {
-        for (int i = threadIdx.x; i < n; i += 1024)
-            if (x[i] > best) best = x[i], idx = i;
-    }
-    bv[threadIdx.x] = best;
-    bi[threadIdx.x] = idx;
-    __syncthreads();
-    for (unsigned s = 512; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            const float ov = bv[threadIdx.x + s];
-            const int oi = bi[threadIdx.x + s];
-            if (ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
-                bv[threadIdx.x] = ov;
-                bi[threadIdx.x] = oi;
-            }
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) *result = bi[0];
-}
-
 template <int GT, int ROPE>
 int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc, int n_q, int n_kv,
                  int seq_len, int64_t ws_floats, float scale, const QkIn& qk, hipStream_t s) {
@@ -638,16 +585,7 @@ int store_kv_launch(void* kcv, void* vcv, const float* k, const float* v, int po
     return launch(store_kv_kernel, dim3(grid_1d(items, 256)), dim3(256), 0, s, kc, vc, k, v, row, kv_dim, vec);
 }
 
-int argmax_launch(const float* x, int* result, int n, hipStream_t s) {
-    if (!x || !result || n < 0 || !aligned(x, 4) || !aligned(result, 4)) return FENCE_ERROR_INVALID_VALUE;
-    return launch(argmax_kernel, dim3(1), dim3(1024), 0, s, result, x, n, aligned(x, 16) ? 1 : 0);
-}
-
 }  // namespace fence
-
-extern "C" int fence_argmax(const float* x, int* result, int n, hipStream_t stream) {
-    return fence::argmax_launch(x, result, n, stream);
-}
 
 extern "C" int fence_gqa_attention(float* attn_out, const float* q, const void* k_cache, const void* v_cache,
                                    int head_dim, int n_q_heads, int n_kv_heads, int seq_len, int max_ctx,

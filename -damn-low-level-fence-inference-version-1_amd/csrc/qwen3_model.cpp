@@ -485,7 +485,13 @@ float* Qwen3Model::forward(int token_id, int pos) {
 
 int Qwen3Model::sample_greedy(float* logits) {
     if (!weight_arena_ || !logits) return fail("no model loaded or no logits", FENCE_ERROR_INVALID_VALUE), -1;
-    const int st = fence_argmax(logits, scratch.argmax_out, config.vocab_size, stream_);
+    // The fused sequence reduces over many workgroups with the partials in
+    // score_buf: attention's scratch, free again once this stream's forward
+    // has run.  Both forms return the reference argmax's index.
+    const int st = sequence_ == Qwen3Sequence::Fused
+                       ? fence_argmax_ws(logits, scratch.argmax_out, config.vocab_size, scratch.score_buf,
+                                         int64_t(kScoreBufScale) * config.n_heads * config.max_ctx * 4, stream_)
+                       : fence_argmax(logits, scratch.argmax_out, config.vocab_size, stream_);
     if (st != FENCE_SUCCESS) return fail(std::string("argmax: ") + fence_status_string(st), st), -1;
     hipError_t e = hipMemcpyAsync(host_token_, scratch.argmax_out, sizeof(int), hipMemcpyDeviceToHost, stream_);
     if (e == hipSuccess) e = hipStreamSynchronize(stream_);

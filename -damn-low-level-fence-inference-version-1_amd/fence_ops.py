@@ -43,6 +43,7 @@ SIGNATURES = {
     "fence_gqa_attention": (_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P),
     "fence_store_kv": (_P, _P, _P, _P, _I, _I, _I, _P),
     "fence_argmax": (_P, _P, _I, _P),
+    "fence_argmax_ws": (_P, _P, _I, _P, _L, _P),
     "fence_residual_add": (_P, _P, _I, _P),
     "fence_f32_to_f16": (_P, _P, _I, _P),
     "fence_f16_to_f32": (_P, _P, _I, _P),
@@ -182,6 +183,10 @@ def store_kv(k_cache, v_cache, k, v, pos, kv_dim, max_ctx, stream=None):
 
 def argmax(x, result, n, stream=None):
     _call("fence_argmax", x, result, n, stream)
+
+
+def argmax_ws(x, result, n, workspace, workspace_bytes, stream=None):
+    _call("fence_argmax_ws", x, result, n, workspace, workspace_bytes, stream)
 
 
 def residual_add(x, residual, n, stream=None):

@@ -145,10 +145,22 @@ int fence_gqa_attention(float* attn_out, const float* q, const void* k_cache,
 int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v,
                    int pos, int kv_dim, int max_ctx, hipStream_t stream);
 
-/* Replaces argmax, src/kernels/ops.cuh:465-505 (greedy sampling):
- * *result = index of the largest of x[0..n), the lowest such index on a tie;
- * NaN never wins; n == 0 gives 0. */
+/* Replaces argmax, src/kernels/ops.cuh:467-505 (greedy sampling):
+ * *result = the index the reference's 256-thread block returns: the largest
+ * of x[0..n) above -1e30 (NaN never wins); on a tie, the thread t = i mod 256
+ * with the smallest 8-bit bit-reversal, then the lowest index (maxima at 1 and
+ * 256 give 256, at 1 and 2 give 2); 0 if nothing is above -1e30 or n == 0.
+ * One workgroup, no scratch memory. */
 int fence_argmax(const float* x, int* result, int n, hipStream_t stream);
+
+/* fence_argmax over many workgroups (same result): the first kernel writes
+ * one 8-byte partial per workgroup into `workspace` (8-byte aligned; up to
+ * 1024 partials, fewer if workspace_bytes is smaller, at least one), a second
+ * one-workgroup kernel reduces them.  The reference's argmax signature has no
+ * scratch argument; a caller that owns a buffer (the model's decode
+ * scratch) uses this form.  EINVAL if workspace is null or under 8 bytes. */
+int fence_argmax_ws(const float* x, int* result, int n, void* workspace, int64_t workspace_bytes,
+                    hipStream_t stream);
 
 /* Replaces residual_add, src/kernels/ops.cuh:265-270: x[i] += residual[i]. */
 int fence_residual_add(float* x, const float* residual, int n, hipStream_t stream);

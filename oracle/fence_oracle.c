@@ -397,14 +397,30 @@ void fo_gqa_attention(float* out, const float* q, const uint16_t* k_cache,
 
 /* src/kernels/ops.cuh:448-480: the largest value; ties go to the lowest index */
 int fo_argmax(const float* x, int n) {
-    float best = -1e30f;
-    int idx = 0;
-    for (int i = 0; i < n; ++i)
-        if (x[i] > best) {
-            best = x[i];
-            idx = i;
-        }
-    return idx;
+    /* src/kernels/ops.cuh:476-485, 256 threads (:502): thread t scans x[t],
+     * x[t+256], .. keeping the first value strictly above its maximum. */
+    enum { THREADS = 256 };
+    float sv[THREADS];
+    int si[THREADS];
+    for (int t = 0; t < THREADS; ++t) {
+        float local_max = -1e30f;
+        int local_idx = 0;
+        for (int i = t; i < n; i += THREADS)
+            if (x[i] > local_max) {
+                local_max = x[i];
+                local_idx = i;
+            }
+        sv[t] = local_max;
+        si[t] = local_idx;
+    }
+    /* ops.cuh:488-498: slot u takes slot u+s only if strictly greater. */
+    for (int s = THREADS / 2; s > 0; s >>= 1)
+        for (int u = 0; u < s; ++u)
+            if (sv[u + s] > sv[u]) {
+                sv[u] = sv[u + s];
+                si[u] = si[u + s];
+            }
+    return si[0];
 }
 
 /* ------------------------------------------------------ fused compositions */

@@ -130,9 +130,12 @@ void fo_store_kv(uint16_t* k_cache, uint16_t* v_cache, const float* k, const flo
 void fo_gqa_attention(float* out, const float* q, const uint16_t* k_cache,
                       const uint16_t* v_cache, int head_dim, int n_q_heads,
                       int n_kv_heads, int seq_len, int max_ctx);
-/* argmax, src/kernels/ops.cuh:448-487 reduced: the first index of the
- * maximum (the reference keeps the first index among a thread's strided
- * elements and the larger value across threads); -1e30 initial maximum. */
+/* argmax, src/kernels/ops.cuh:467-505, as the reference's one 256-thread
+ * block computes it: thread t keeps the first strict maximum of x[t],
+ * x[t+256], .. (initial -1e30f, index 0), then a tree over s = 128 .. 1 in
+ * which slot u takes slot u+s only if strictly greater.  A tie across
+ * threads goes to the thread with the smallest 8-bit bit-reversal, which is
+ * not always the lowest index (maxima at 1 and 256 give 256). */
 int fo_argmax(const float* x, int n);
 
 /* IEEE binary32 -> binary16, round to nearest, ties to even; overflow -> inf;

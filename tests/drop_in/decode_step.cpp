@@ -445,6 +445,9 @@ int check_mode() {
     argmax(s.logits, s.argmax_out, V);
     const auto tok = get(s.argmax_out, 1);
     report("argmax(logits)", tok[0] == fo_argmax(dl.data(), V), 0);
+    fence_argmax_ws(s.logits, s.argmax_out, V, s.score_buf, 16 * int64_t(NQ) * CTX, nullptr);
+    const auto tok_ws = get(s.argmax_out, 1);
+    report("argmax over many workgroups (fence_argmax_ws)", tok_ws[0] == tok[0], 0);
 
     std::printf("%d/%d passed\n", g_pass, g_pass + g_fail);
     free_layer(L);
@@ -480,7 +483,7 @@ int time_mode(int n_layers, int pos, bool with_graph) {
         for (auto& L : layers) layer_fused(L, s, pos, st);
         fence_residual_rms_norm_f16(s.hidden, s.tmp, out_norm, s.normed, s.x_half, 1, E, EPS, st);
         fence_gemv_q8_0(table, s.normed, s.logits, V, E, st);
-        fence_argmax(s.logits, s.argmax_out, V, st);
+        fence_argmax_ws(s.logits, s.argmax_out, V, s.score_buf, 16 * int64_t(NQ) * CTX, st);
     };
     hipEvent_t e0, e1;
     HIP_CHECK(hipEventCreate(&e0));
@@ -513,7 +516,7 @@ int time_mode(int n_layers, int pos, bool with_graph) {
     for (auto& L : layers) layer_fused(L, s, pos, st);
     fence_residual_rms_norm_f16(s.hidden, s.tmp, out_norm, s.normed, s.x_half, 1, E, EPS, st);
     fence_gemv_q8_0(table, s.normed, s.logits, V, E, st);
-    fence_argmax(s.logits, s.argmax_out, V, st);
+    fence_argmax_ws(s.logits, s.argmax_out, V, s.score_buf, 16 * int64_t(NQ) * CTX, st);
     HIP_CHECK(hipStreamEndCapture(st, &graph));
     HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
     us_graph = time_it([&](int) { HIP_CHECK(hipGraphLaunch(exec, st)); }, 3, 10);

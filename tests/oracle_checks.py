@@ -583,14 +583,75 @@ def check_attention(o: Oracle):
           np.array_equal(np.delete(vc2, 7, 0), np.delete(vc, 7, 0)))
     if not ok:
         fails.append("store_kv: row pos is not binary16(k), binary16(v), or other rows changed")
-    # argmax: first index of the maximum, NaN never wins
-    x = rng.standard_normal(1000).astype(np.float32)
-    x[[10, 700]] = 9.0
-    x[3] = np.nan
-    if o.argmax(x) != 10:
-        fails.append("argmax: not the first index of the maximum")
-    if o.argmax(np.full(5, -np.inf, np.float32)) != 0:
-        fails.append("argmax of all -inf is not 0")
+    fails += check_argmax(o, rng)
+    return fails
+
+
+def rev8(v: int) -> int:
+    return int(f"{v:08b}"[::-1], 2)
+
+
+def argmax_closed_form(x: np.ndarray) -> int:
+    """The reference argmax's result (src/kernels/ops.cuh:467-505) without
+    simulating its block: among the indices holding the largest value above
+    -1e30f (NaN never qualifies; -0 == +0), the least (rev8(i mod 256), i);
+    0 if none qualifies.  Derivation: thread t = i mod 256 keeps its first
+    strict maximum, and tree level s pairs slots that differ in bit log2(s),
+    the lower slot keeping an equal value."""
+    x = np.asarray(x, np.float32)
+    cand = np.nonzero(x > np.float32(-1e30))[0]
+    if cand.size == 0:
+        return 0
+    m = x[cand].max()
+    tied = cand[x[cand] == m]
+    return int(min(tied, key=lambda i: (rev8(int(i) % 256), int(i))))
+
+
+def check_argmax(o: Oracle, rng):
+    fails = []
+    base = np.full(1000, -1.0, np.float32)
+
+    def with_max(idx, n=1000, val=9.0):
+        x = base[:n].copy() if n <= 1000 else np.full(n, -1.0, np.float32)
+        x[list(idx)] = val
+        return x
+    # hand-derived tie cases of the 256-thread block
+    for idx, want in (((1, 256), 256), ((1, 2), 2), ((0, 255), 0), ((10, 700), 700), ((256, 512), 256),
+                      ((3, 259), 3), ((127, 129), 129), ((999,), 999)):
+        if o.argmax(with_max(idx)) != want:
+            fails.append(f"argmax: maxima at {idx} do not give {want}")
+    # NaN never wins; nothing above -1e30 gives 0; n == 0 gives 0
+    x = with_max((700,))
+    x[[3, 900]] = np.nan
+    if o.argmax(x) != 700:
+        fails.append("argmax: a NaN won")
+    for fill in (-np.inf, np.nan, np.float32(-1e30), -2e30):
+        if o.argmax(np.full(600, fill, np.float32)) != 0:
+            fails.append(f"argmax of all {fill} is not 0")
+    x = np.full(600, -2e30, np.float32)
+    x[5] = -1.5e30
+    if o.argmax(x) != 0:
+        fails.append("argmax: a value below -1e30 qualified")
+    if o.argmax(np.zeros(0, np.float32)) != 0:
+        fails.append("argmax of an empty vector is not 0")
+    # -0 and +0 tie: same thread keeps the first, across threads the tree decides
+    x = with_max((), val=0)
+    x[3], x[259] = -0.0, 0.0
+    if o.argmax(x) != 3:
+        fails.append("argmax: -0 then +0 in one thread does not keep the first")
+    x = with_max(())
+    x[1], x[2] = 0.0, -0.0
+    if o.argmax(x) != 2:
+        fails.append("argmax: +0 at 1 and -0 at 2 do not tie")
+    # many ties at many lengths against the closed form
+    for n in (1, 7, 255, 256, 257, 1000, 4099, 151936):
+        for trial in range(3):
+            x = rng.integers(-20, 3 if trial < 2 else 40, n).astype(np.float32)
+            if trial == 1:
+                x[rng.integers(0, n, max(1, n // 50))] = np.nan
+            if o.argmax(x) != argmax_closed_form(x):
+                fails.append(f"argmax n={n} trial {trial}: differs from the closed form")
+                break
     return fails
 
 

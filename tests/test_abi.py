@@ -125,6 +125,12 @@ def _raw(name):
     ("fence_store_kv", (16, 32, 48, 64, 100, 512, 100, None)),                # pos == max_ctx
     ("fence_store_kv", (16, 32, 48, 64, -1, 512, 100, None)),
     ("fence_argmax", (16, None, 10, None)),
+    ("fence_argmax", (BAD, 32, 10, None)),
+    ("fence_argmax", (16, 32, -1, None)),
+    ("fence_argmax_ws", (16, 32, 10, None, 64, None)),           # no workspace
+    ("fence_argmax_ws", (16, 32, 10, 48, 7, None)),              # under one partial
+    ("fence_argmax_ws", (16, 32, 10, 0x1004, 64, None)),         # workspace not 8-byte aligned
+    ("fence_argmax_ws", (16, None, 10, 48, 64, None)),
     ("fence_residual_add", (16, None, 8, None)),
     ("fence_residual_add", (BAD, 32, 8, None)),
     ("fence_f32_to_f16", (0x1001, 32, 8, None)),                  # binary16 output not 2-byte aligned

@@ -38,6 +38,7 @@ def test_drop_in_decode_layer():
 def test_drop_in_decode_step_stages():
     out = run([STEP])
     assert "PASS argmax(logits)" in out
+    assert "PASS argmax over many workgroups (fence_argmax_ws)" in out
 
 
 @pytest.mark.gpu

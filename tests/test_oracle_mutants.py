@@ -52,7 +52,10 @@ MUTANTS = [
     ("attn_scale_1_over_d", "const float scale = 1.0f / sqrtf((float)head_dim);", "const float scale = 1.0f / (float)head_dim;"),
     ("attn_v_stride", "v_cache[t * kv_dim + (int64_t)kvh * head_dim + d]", "v_cache[t * head_dim + (int64_t)kvh * head_dim + d]"),
     ("store_kv_wrong_row", "k_cache[(int64_t)pos * kv_dim + i] = fo_f32_to_f16(k[i]);", "k_cache[(int64_t)(pos + 1) * kv_dim + i] = fo_f32_to_f16(k[i]);"),
-    ("argmax_last_tie", "if (x[i] > best) {", "if (x[i] >= best) {"),
+    ("argmax_last_tie", "if (x[i] > local_max) {", "if (x[i] >= local_max) {"),
+    ("argmax_tree_upper_slot_wins_ties", "if (sv[u + s] > sv[u]) {", "if (sv[u + s] >= sv[u]) {"),
+    ("argmax_1024_threads", "enum { THREADS = 256 };", "enum { THREADS = 1024 };"),
+    ("argmax_initial_minus_inf", "float local_max = -1e30f;", "float local_max = -INFINITY;"),
     ("qk_norm_k_uses_q_weight", "fo_rms_norm_per_head(k + t * krow, wk,", "fo_rms_norm_per_head(k + t * krow, wq,"),
 ]
 
