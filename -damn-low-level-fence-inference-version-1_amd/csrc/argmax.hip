@@ -25,6 +25,8 @@
 // keys once, at the end.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace fence {
 namespace {
 
@@ -168,6 +170,55 @@ int argmax_ws_launch(const float* x, int* result, int n, void* workspace, int64_
     return argmax_parts_launch(x, result, n, static_cast<uint64_t*>(workspace), count, s);
 }
 
+// ------------------------------------------------- allocation-free variant
+//
+// fence_argmax_noalloc keeps its partials in `scratch`, a file-scope device
+// array: kArgmaxMaxParts keys, 8 KiB.  Every GPU the library runs on holds its
+// own copy until the process ends, and every call on one GPU shares it, so
+// calls that overlap on one GPU (two streams, two threads) race; calls
+// ordered on one stream do not.  Nothing in it must start at zero: each call's
+// first kernel writes every partial its second kernel reads.  In host code the
+// array's name is not a device address, so the address each device gives for
+// it (hipGetSymbolAddress, once per device, with that device current) is what
+// the kernels get.
+
+namespace {
+
+static __device__ __align__(256) uint64_t scratch[kArgmaxMaxParts];
+
+constexpr int kMaxDevices = 64;
+uint64_t* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// This device's address of `scratch`, looked up on the device's first call.
+int scratch_ptr(uint64_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= kMaxDevices) return FENCE_ERROR_INVALID_VALUE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (!p) return FENCE_ERROR_INVALID_VALUE;
+        g_scratch_ptr[dev] = static_cast<uint64_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return FENCE_SUCCESS;
+}
+
+}  // namespace
+
+int argmax_noalloc_launch(const float* x, int* result, int n, hipStream_t s) {
+    if (!x || !result || n < 0 || !aligned(x, 4) || !aligned(result, 4)) return FENCE_ERROR_INVALID_VALUE;
+    uint64_t* parts = nullptr;
+    const int st = scratch_ptr(&parts);
+    if (st != FENCE_SUCCESS) return st;
+    // every n fits: the grid is capped at kArgmaxMaxParts workgroups
+    return argmax_parts_launch(x, result, n, parts, argmax_parts(n, kArgmaxMaxParts), s);
+}
+
 }  // namespace fence
 
 extern "C" int fence_argmax(const float* x, int* result, int n, hipStream_t stream) {
@@ -179,3 +230,6 @@ extern "C" int fence_argmax_ws(const float* x, int* result, int n, void* workspa
     return fence::argmax_ws_launch(x, result, n, workspace, workspace_bytes, stream);
 }
 
+extern "C" int fence_argmax_noalloc(const float* x, int* result, int n, hipStream_t stream) {
+    return fence::argmax_noalloc_launch(x, result, n, stream);
+}

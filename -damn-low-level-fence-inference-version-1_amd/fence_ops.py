@@ -44,6 +44,7 @@ SIGNATURES = {
     "fence_store_kv": (_P, _P, _P, _P, _I, _I, _I, _P),
     "fence_argmax": (_P, _P, _I, _P),
     "fence_argmax_ws": (_P, _P, _I, _P, _L, _P),
+    "fence_argmax_noalloc": (_P, _P, _I, _P),
     "fence_residual_add": (_P, _P, _I, _P),
     "fence_f32_to_f16": (_P, _P, _I, _P),
     "fence_f16_to_f32": (_P, _P, _I, _P),
@@ -187,6 +188,10 @@ def argmax(x, result, n, stream=None):
 
 def argmax_ws(x, result, n, workspace, workspace_bytes, stream=None):
     _call("fence_argmax_ws", x, result, n, workspace, workspace_bytes, stream)
+
+
+def argmax_noalloc(x, result, n, stream=None):
+    _call("fence_argmax_noalloc", x, result, n, stream)
 
 
 def residual_add(x, residual, n, stream=None):

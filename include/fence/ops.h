@@ -162,6 +162,16 @@ int fence_argmax(const float* x, int* result, int n, hipStream_t stream);
 int fence_argmax_ws(const float* x, int* result, int n, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): fence_argmax_ws with its partials in the library's own
+ * static device scratch (8 KiB, up to 1024 partials; every n fits) instead of
+ * a workspace.  Allocates nothing.  Each GPU holds one scratch for the life of
+ * the process and every call on that GPU shares it: calls that overlap on one
+ * GPU (two streams or threads at once) race; calls ordered on one stream do
+ * not.  Same index as fence_argmax. */
+int fence_argmax_noalloc(const float* x, int* result, int n, hipStream_t stream);
+
 /* Replaces residual_add, src/kernels/ops.cuh:265-270: x[i] += residual[i]. */
 int fence_residual_add(float* x, const float* residual, int n, hipStream_t stream);
 

@@ -131,6 +131,8 @@ def _raw(name):
     ("fence_argmax_ws", (16, 32, 10, 48, 7, None)),              # under one partial
     ("fence_argmax_ws", (16, 32, 10, 0x1004, 64, None)),         # workspace not 8-byte aligned
     ("fence_argmax_ws", (16, None, 10, 48, 64, None)),
+    ("fence_argmax_noalloc", (None, 32, 10, None)),
+    ("fence_argmax_noalloc", (16, 32, -1, None)),
     ("fence_residual_add", (16, None, 8, None)),
     ("fence_residual_add", (BAD, 32, 8, None)),
     ("fence_f32_to_f16", (0x1001, 32, 8, None)),                  # binary16 output not 2-byte aligned
