@@ -188,6 +188,10 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
                 }
             }
         }
+        // A masked slot's clamped row may be the one this launch is writing
+        // (position 0) or hold any bits; its weight is 0, and so is its V.
+#pragma unroll
+        for (int i = 0; i < kPPG; ++i) vr[i] = on[i] ? vr[i] : h8(0);
         // (A) scores, in log2 units
         float(&spb)[GT][kSub] = sp[sub & 1];
 #pragma unroll

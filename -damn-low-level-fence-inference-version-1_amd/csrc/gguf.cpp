@@ -244,9 +244,20 @@ void GGUFFile::parse() {
 
     for (auto& ti : tensors_) {
         const GGMLTypeInfo info = ggml_type_info(ti.type);
-        // element count with overflow detection (dims come from the file)
+        // Element count, each multiply checked before it is made (the dims
+        // come from the file).  2^72 elements need more than 2^64 bytes in
+        // every type (a block of at most 256 elements takes at least one
+        // byte), so no file holds them; capping n there keeps it and the byte
+        // count below far from wrapping, and the end-of-file check rejects
+        // the rest.
+        const unsigned __int128 max_n = static_cast<unsigned __int128>(1) << 72;
         unsigned __int128 n = 1;
-        for (uint32_t d = 0; d < ti.n_dims; ++d) n *= ti.dims[d];
+        for (uint32_t d = 0; d < ti.n_dims; ++d) {
+            const uint64_t dim = ti.dims[d];
+            if (dim != 0 && n > max_n / dim)
+                throw ParseError("tensor '" + ti.name + "' has more elements than the file could hold");
+            n *= dim;
+        }
         const unsigned __int128 bytes = (n + info.block_size - 1) / info.block_size * info.type_size;
         const unsigned __int128 start = static_cast<unsigned __int128>(data_offset_) + ti.offset;
         if (start >= file_size_)

@@ -234,6 +234,11 @@ def test_rejects_malformed_tensor_infos(tmp_path):
     # data running past the end: rejected here (the reference checks the first byte only)
     write_gguf(p, [], [("t", [1000], F32, b"\0" * 16)])
     assert "past the end" in _bad(p)
+    # dims whose product wraps 128 bits to 0 (2^43 * 2^43 * 2^42 = 2^128): caught before the wrap
+    write_gguf(p, [], [("t", [1 << 43, 1 << 43, 1 << 42], F32, b"\0" * 16)])
+    assert "more elements than the file" in _bad(p)
+    write_gguf(p, [], [("t", [1 << 40, 1 << 40], Q8_0, b"\0" * 34)])
+    assert "more elements than the file" in _bad(p)
 
 
 def test_rejects_counts_and_lengths_beyond_the_file(tmp_path):

@@ -59,11 +59,19 @@ def test_reader_under_sanitizers_on_corrupted_files(tmp_path):
         p = tmp_path / f"bad{trial}.gguf"
         p.write_bytes(bytes(b))
         files.append(str(p))
-    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:halt_on_error=1",
+    # ASan normally insists on coming first in the library list; the process
+    # environment may preload another library, which is left as it is
+    env = dict(os.environ,
+               ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:halt_on_error=1:verify_asan_link_order=0",
                UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
-    env.pop("LD_PRELOAD", None)
     r = subprocess.run([str(exe)] + files, capture_output=True, text=True, errors="replace", timeout=300, env=env)
     assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-4000:])
     assert "ERROR: AddressSanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-4000:]
     opened = int(r.stdout.split("opened ")[1].split()[0])
     assert opened >= 1  # the valid file at least
+    # dims whose element count wraps 128 bits (2^43 * 2^43 * 2^42 = 2^128, so a
+    # wrapping count would read 0 elements): rejected, under the sanitizers
+    wrap = tmp_path / "wrap.gguf"
+    write_gguf(wrap, [], [("t", [1 << 43, 1 << 43, 1 << 42], F32, b"\0" * 16)])
+    r = subprocess.run([str(exe), str(wrap)], capture_output=True, text=True, errors="replace", timeout=60, env=env)
+    assert r.returncode == 0 and "opened 0 rejected 1" in r.stdout, (r.stdout, r.stderr[-2000:])

@@ -1,10 +1,15 @@
 """GPU parity of decode attention (fence_gqa_attention) and the KV store
 (fence_store_kv) against the oracle, through the C ABI.
 
-Attention bar (fp32): per query head, max|out - out_oracle| <= 1e-5 * the
-largest |v| among the head's attended V rows -- the output is a convex
-combination of those rows, so that is its natural scale.  One attended
-position must give that V row exactly.  The KV store is exact.
+Attention bars (fp32), per query head:
+  * max|out - out_oracle| <= 1e-5 * the largest |v| among the head's attended
+    V rows -- the output is a convex combination of those rows -- on every
+    case;
+  * and, at the decode lengths of the configs (2915 and 4096 positions) for
+    all three entry points (fence_gqa_attention, _f16, _qk_f16),
+    max|out - out_oracle| <= 1e-5 * max|out_oracle| of that head: the output's
+    own scale, which is ~80x smaller there (random V averages out).
+One attended position must give that V row exactly.  The KV store is exact.
 """
 import numpy as np
 import pytest
@@ -137,3 +142,53 @@ def test_store_then_attend(oracle):
     rk, rv = oracle.store_kv(kc, vc, k, v, pos)
     assert_attention(host(out), oracle.gqa_attention(q, rk, rv, n_q, n_kv, hd, pos + 1), rv, n_q, n_kv, hd,
                      pos + 1, "store then attend")
+
+
+def out_scale_ratio(got, ref, n_q, hd):
+    """Per head max|got - ref| / max|ref|; the worst head's ratio."""
+    g = np.asarray(got, np.float64).reshape(n_q, hd)
+    r = np.asarray(ref, np.float64).reshape(n_q, hd)
+    return float(np.max(np.max(np.abs(g - r), axis=1) / np.max(np.abs(r), axis=1)))
+
+
+@pytest.mark.parametrize("variant", ["plain", "f16", "qk_f16"])
+@pytest.mark.parametrize("seq", [2915, 4096])
+def test_attention_bar_relative_to_output(oracle, variant, seq):
+    """The tighter bar, relative to each head's own output scale, for the
+    three attention entry points at the configs' decode lengths."""
+    torch = torch_mod()
+    n_q, n_kv, hd, ctx = 32, 8, 128, 4096
+    rng = np.random.default_rng(seq + len(variant))
+    kc, vc = caches(rng, ctx, n_kv, hd)
+    q = (rng.standard_normal(n_q * hd) * 0.3).astype(np.float32)
+    ws = torch.empty(4 * n_q * ctx, device="cuda")
+    o32 = torch.full((n_q * hd,), float("nan"), device="cuda")
+    o16 = torch.full((n_q * hd,), -1, dtype=torch.int16, device="cuda")
+    LIVE.extend([ws, o32, o16])
+    kd, vd = dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    if variant == "plain":
+        F.gqa_attention(o32.data_ptr(), dev(q).data_ptr(), kd.data_ptr(), vd.data_ptr(), hd, n_q, n_kv, seq, ctx,
+                        ws.data_ptr(), stream())
+        ref = oracle.gqa_attention(q, kc, vc, n_q, n_kv, hd, seq)
+    elif variant == "f16":
+        F.gqa_attention_f16(o32.data_ptr(), o16.data_ptr(), dev(q).data_ptr(), kd.data_ptr(), vd.data_ptr(), hd,
+                            n_q, n_kv, seq, ctx, ws.data_ptr(), 4 * n_q * ctx, stream())
+        ref = oracle.gqa_attention(q, kc, vc, n_q, n_kv, hd, seq)
+    else:  # q/k prologue: QK-norm + NeoX RoPE of q and of the new k at pos = seq - 1, stored, then attended
+        pos = seq - 1
+        k = rng.standard_normal(n_kv * hd).astype(np.float32)
+        v = rng.standard_normal(n_kv * hd).astype(np.float32)
+        wq = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+        wk = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+        F.gqa_attention_qk_f16(o32.data_ptr(), o16.data_ptr(), dev(q).data_ptr(), dev(k).data_ptr(),
+                               dev(v).data_ptr(), dev(wq).data_ptr(), dev(wk).data_ptr(), kd.data_ptr(),
+                               vd.data_ptr(), hd, n_q, n_kv, pos, ctx, 1e-6, 1e6, F.ROPE_NEOX, ws.data_ptr(),
+                               4 * n_q * ctx, stream())
+        rq, rk = oracle.qk_norm_rope(q.reshape(1, n_q, hd), k.reshape(1, n_kv, hd), wq, wk, 1e-6, None, pos, 1e6,
+                                     F.ROPE_NEOX)
+        rkc, rvc = oracle.store_kv(kc, vc, rk.reshape(-1), v, pos)
+        ref = oracle.gqa_attention(rq.reshape(-1), rkc, rvc, n_q, n_kv, hd, seq)
+    got = host(o32)
+    ratio = out_scale_ratio(got, ref, n_q, hd)
+    print(f"attention {variant} seq {seq}: worst head max|err| / max|out| = {ratio:.3g}")
+    assert ratio <= TOL, f"{variant} seq {seq}: {ratio:.3g} of the output's scale"

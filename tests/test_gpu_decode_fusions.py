@@ -233,6 +233,24 @@ def test_attention_qk_equals_head_ops_then_attention(oracle, nq, nkv, hd, pos, c
             assert np.max(np.abs(gq[h] - ref_o[h])) <= 1e-5 * V[:, h // (nq // nkv), :].max() + 2e-6, f"head {h}"
 
 
+def test_attention_qk_first_position_nan_cache():
+    """Position 0 with a cache full of NaN bits: the one key is the new row,
+    written by this launch; no masked slot may carry a NaN into the output.
+    Bit for bit the two calls' result, and finite."""
+    rng = np.random.default_rng(31)
+    nq, nkv, hd, ctx = 32, 8, 128, 4096
+    q, k, v, wq, wk, kc, vc = attention_qk_operands(rng, nq, nkv, hd, ctx, True)
+    kc[:] = 0x7E00  # binary16 quiet NaN everywhere
+    vc[:] = 0x7E00
+    ops = (q, k, v, wq, wk, kc, vc)
+    got = run_attention_qk(ops, nq, nkv, hd, 0, 1e6, F.ROPE_NEOX, 4 * nq * ctx, fused=True)
+    ref = run_attention_qk(ops, nq, nkv, hd, 0, 1e6, F.ROPE_NEOX, 4 * nq * ctx, fused=False)
+    assert np.all(np.isfinite(got[0])) and np.all(np.isfinite(ref[0]))
+    for g, r, what in zip(got, ref, ("fp32 out", "binary16 out", "k cache", "v cache")):
+        assert np.array_equal(g.view(np.uint32 if g.dtype == np.float32 else np.uint16),
+                              r.view(np.uint32 if r.dtype == np.float32 else np.uint16)), what
+
+
 def test_attention_qk_rejects_bad_arguments():
     torch = torch_mod()
     nq, nkv, hd, ctx = 8, 2, 128, 64
