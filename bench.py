@@ -453,16 +453,18 @@ def measure_configs(torch, F, reps, extended):
 
     scrub = {"buf": None}
 
-    def measure(cfg, key, name, nbytes, make_set, run, kernel, note="", launches=1):
+    def measure(cfg, key, name, nbytes, make_set, run, kernel, note="", launches=1, warm=False):
         """launches: kernels the call runs; the timing spans the first one's
-        start to the last one's end."""
+        start to the last one's end.  warm: one buffer set, no eviction."""
         probe = make_set()
         sb = sum(t.numel() * t.element_size() for t in probe.values() if torch.is_tensor(t))
-        small = sb < (16 << 20)
-        sets = [probe] + [make_set() for _ in range(1 if small else nsets_for(sb) - 1)]
+        small = sb < (1 << 20) and not warm
+        nsets = 1 if warm else (2 if small else nsets_for(sb))
+        sets = [probe] + [make_set() for _ in range(nsets - 1)]
         if small and scrub["buf"] is None:
             scrub["buf"] = torch.empty((1 << 30) // 4, **dev)
-        for i in range(3):
+        # every set once before timing: no timed launch is the first touch of its buffers
+        for i in range(max(3, len(sets))):
             run(sets[i % len(sets)])
         evs = [(hev.create(), hev.create()) for _ in range(reps)]
         for i in range(reps):
@@ -474,7 +476,8 @@ def measure_configs(torch, F, reps, extended):
         r = summarize([hev.elapsed_ms(a, b) * 1e3 for a, b in evs], nbytes, kernel)
         hev.destroy_all()
         r = {"config": cfg, "key": key, "op": name, **r, "launches_per_call": launches, "sets": len(sets),
-             "cold": "1 GiB scrub between launches" if small else "rotating buffer sets"}
+             "cold": "warm (one set)" if warm else ("1 GiB scrub between launches" if small else
+                                                    "rotating buffer sets")}
         if note:
             r["note"] = note
         results.append(r)
@@ -487,6 +490,12 @@ def measure_configs(torch, F, reps, extended):
         return torch.randn(*shape, **dev, generator=gen)
 
     h16 = dict(dtype=torch.int16, device="cuda")
+
+    # The per-launch floor: a launch that moves one float4 per stream, warm.
+    measure("floor", "swiglu_one_float4", "swiglu n=4 (one float4: the per-launch floor)", 48,
+            lambda: dict(g=randn(4), u=randn(4), o=torch.empty(4, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), 4, sh),
+            "swiglu_vec_kernel", warm=True)
 
     # ---- Qwen3-4B decode, one token, fp32
     E0, F0, V0 = 2560, 9728, 151936
