@@ -8,8 +8,11 @@
 //   freq[p] = 1.0f / powf(base, (float)(2p)/(float)hd)    (ops.cuh:133),
 //   a = (float)pos * freq[p];  x0' = x0 cos a - x1 sin a;  x1' = x0 sin a + x1 cos a.
 //
-// Layout of the vector kernel: one workgroup (up to 16 waves) per token.  A token's q and k
-// heads are cut into "units" of 8 floats, elements [4i, 4i+4) and
+// Two vector kernels.  The streaming kernel (head_dim 128, no row norm, no
+// KV store) gives each lane one float4 and each one-wave workgroup two heads
+// of a token.  The unit kernel covers the rest, one workgroup (up to 16
+// waves) per token: a token's q and k heads are cut into "units" of 8
+// floats, elements [4i, 4i+4) and
 // [hd/2 + 4i, hd/2 + 4i + 4) of one head (i < hd/8), so a lane holds four
 // whole NeoX pairs -- or four whole interleaved pairs -- and never needs a
 // partner lane.  A head is hd/8 consecutive lanes, so the per-head sum of
@@ -299,6 +302,82 @@ __global__ __launch_bounds__(256) void head_ops_scalar_kernel(const HeadArgs arg
     }
 }
 
+// One float4 per lane, one wave per workgroup: two heads (head_dim 128) of
+// one token, 32 lanes per head -- the streaming shape that moves an in-place
+// 1-read/1-write array fastest (one float4 per lane, one-wave workgroups;
+// a plain in-place stream probe reaches 84% of peak this way against 81% with
+// two float4 per lane).  It takes RoPE alone, per-head norm and per-head
+// norm -> RoPE (no row norm, no KV store): in-process A/B, p50, configs[4]
+// RoPE 54.03 -> 52.19 us, configs[2] QK-norm -> RoPE 28.44 -> 27.12 us.
+// The arithmetic is the unit kernel's, operation for operation, so results
+// are bit-identical: a NeoX partner (hd/2 away) comes from lane l ^ 16 by a
+// swizzle; the per-head sum of squares first adds the two halves of a unit
+// in the unit kernel's order (first half + second half), then runs the same
+// 16-lane DPP tree.  Q heads come first in the grid, then K heads.
+template <int ROPE, int NORM>
+__global__ __launch_bounds__(64) void head_stream_kernel(const HeadArgs args, InvFreq tab, int64_t wg_q) {
+    constexpr int HD = 128, HALF = 64;
+    __shared__ __align__(16) float cs[2 * HALF];
+    const int lane = threadIdx.x;
+    const int ii = lane & 31;  // float4 of the head: elements [4 ii, 4 ii + 4)
+    const int64_t w = blockIdx.x;
+    const bool isq = w < wg_q;  // workgroup-uniform
+    const int nh = isq ? args.nq : args.nkv;
+    const int64_t g = 2 * (isq ? w : w - wg_q) + (lane >> 5);  // head in [tokens][nh]
+    const int64_t t = (2 * (isq ? w : w - wg_q)) / nh;         // both heads of the workgroup: one token
+    const float* src = isq ? args.qi + g * HD : args.k + g * HD;
+    float* dst = isq ? args.qo + g * HD : args.k + g * HD;
+    f4 v = ld4<true>(src + 4 * ii);
+    f4 wv = f4(1.0f);
+    if constexpr (NORM == kNormHead) wv = ld4<false>((isq ? args.wq : args.wk) + 4 * ii);
+    if constexpr (ROPE != kRopeNone) {
+        const int pos = args.positions ? args.positions[t] : args.pos0 + static_cast<int>(t);
+        float sn, cn;
+        sincos_angle(static_cast<float>(pos) * tab.v[lane], &sn, &cn);
+        cs[lane] = cn;
+        cs[HALF + lane] = sn;
+    }
+    if constexpr (NORM == kNormHead) {
+        // the unit kernel's dot4(a) + dot4(b), a the first half, then its 16-lane tree
+        const float s = dot4(v);
+        const float sp = swz_xor16(s);
+        const float u = ii < 16 ? s + sp : sp + s;
+        const float tot = group_reduce<16>(u, OpAdd{});
+        const float r = head_rscale(tot, static_cast<float>(HD), args.eps);
+        v = (wv * v) * r;
+    }
+    if constexpr (ROPE != kRopeNone) {
+        __syncthreads();  // cs
+        if constexpr (ROPE == kRopeNeox) {
+            f4 o;
+            o.x = swz_xor16(v.x), o.y = swz_xor16(v.y), o.z = swz_xor16(v.z), o.w = swz_xor16(v.w);
+            const int p = 4 * (ii & 15);
+            const f4 c = *reinterpret_cast<const f4*>(cs + p);
+            const f4 sn = *reinterpret_cast<const f4*>(cs + HALF + p);
+            if (ii < 16) {  // x0 = v, x1 = partner: x0 c - x1 s
+                v = f4{rope_pair(v.x, o.x, c.x, sn.x).x, rope_pair(v.y, o.y, c.y, sn.y).x,
+                       rope_pair(v.z, o.z, c.z, sn.z).x, rope_pair(v.w, o.w, c.w, sn.w).x};
+            } else {  // x0 = partner, x1 = v: x0 s + x1 c
+                v = f4{rope_pair(o.x, v.x, c.x, sn.x).y, rope_pair(o.y, v.y, c.y, sn.y).y,
+                       rope_pair(o.z, v.z, c.z, sn.z).y, rope_pair(o.w, v.w, c.w, sn.w).y};
+            }
+        } else {  // interleaved: pairs 2 ii and 2 ii + 1 inside the float4
+            const f2 c = *reinterpret_cast<const f2*>(cs + 2 * ii);
+            const f2 sn = *reinterpret_cast<const f2*>(cs + HALF + 2 * ii);
+            const f2 a0 = rope_pair(v.x, v.y, c.x, sn.x), a1 = rope_pair(v.z, v.w, c.y, sn.y);
+            v = f4{a0.x, a0.y, a1.x, a1.y};
+        }
+    }
+    st4<true>(dst + 4 * ii, v);
+}
+
+template <int ROPE, int NORM>
+int launch_stream(const HeadArgs& a, const InvFreq& tab, hipStream_t s) {
+    const int64_t wg_q = a.tokens * a.nq / 2, wg_k = a.tokens * a.nkv / 2;
+    return launch(head_stream_kernel<ROPE, NORM>, dim3(static_cast<unsigned>(wg_q + wg_k)), dim3(64), 0, s, a,
+                  tab, wg_q);
+}
+
 template <int ROPE, int NORM, int G, bool KV>
 int dispatch_slots(unsigned grid, unsigned threads, hipStream_t s, const HeadArgs& a, int slots,
                    const InvFreq& tab) {
@@ -322,6 +401,11 @@ template <int ROPE, int NORM>
 int dispatch(bool vec, int G, unsigned grid, unsigned threads, hipStream_t s, const HeadArgs& a, int hd,
              int slots, const InvFreq& tab) {
     if (!vec) return launch(head_ops_scalar_kernel<ROPE, NORM>, dim3(grid), dim3(256), 0, s, a, hd, tab);
+    if constexpr (NORM != kNormRow) {
+        if (G == 16 && !a.kc && a.nq % 2 == 0 && a.nkv % 2 == 0 &&
+            a.tokens * (a.nq + a.nkv) / 2 < (int64_t(1) << 31))
+            return launch_stream<ROPE, NORM>(a, tab, s);
+    }
     if constexpr (ROPE != kRopeNone && NORM != kNormRow) {  // the KV store follows a RoPE
         if (a.kc) return dispatch_vec<ROPE, NORM, true>(G, grid, threads, s, a, slots, tab);
     }
@@ -404,7 +488,13 @@ int head_ops_launch(float* qo, const float* qi, float* k, const float* wq, const
                ok16(wq) && ok16(wk) && ok16(kc) && ok16(vc) && ok16(v);
     unsigned threads = 256;
     int slots = 0;
-    if (vec) vec = plan_row(tokens, static_cast<int64_t>(nq + nkv) * G, FENCE_HEAD_SLOTS, 2, &threads, &slots);
+    // Units per lane: RoPE alone streams best with one (two float4 per lane:
+    // 8192 tokens x 40 heads, p50 54.75 -> 53.99 us, in-process A/B); with a
+    // norm two, which halve the lanes that reduce (QK-norm -> RoPE at 4096
+    // tokens 28.44 us with two, 30.20 with one).  plan_row halves the target
+    // anyway when the tokens cannot fill the GPU.
+    const int target = norm == kNormNone ? 1 : FENCE_HEAD_SLOTS;
+    if (vec) vec = plan_row(tokens, static_cast<int64_t>(nq + nkv) * G, target, 2, &threads, &slots);
     const unsigned grid = grid_1d(tokens, 1, 1 << 20);
     const HeadArgs a{qo, qi, k, wq, wk, tokens, nq, nkv, eps, positions, pos0, kc, vc, v, max_ctx};
     switch (rope) {

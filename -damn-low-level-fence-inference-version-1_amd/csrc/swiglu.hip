@@ -4,10 +4,13 @@
 // Follows silu_elementwise_mul, src/kernels/ops.cuh:183-202:
 //   out[i] = (g / (1.0f + expf(-g))) * up[i],  g = gate[i].
 // Streaming kernel: one float4 of gate and one of up per lane, non-temporal
-// 128-bit loads and stores.  Measured on MI355X, more float4s per lane (a
-// deeper unroll) lowers the achieved bandwidth -- 8 per lane per stream
-// halves it -- while many shallow waves reach 72% of peak at 29 MB per
-// stream and 82% at 470 MB.
+// 128-bit loads and stores, one-wave workgroups.  Measured on MI355X, more
+// float4s per lane (a deeper unroll) lowers the achieved bandwidth -- 8 per
+// lane per stream halves it -- while many shallow waves reach 72% of peak at
+// 29 MB per stream and 82% at 470 MB with 256-thread workgroups, 84% with
+// 64-thread ones (in-process A/B, p50: 8192 x 14336 216.5 -> 209.9 us,
+// 4096 x 12288 93.9 -> 90.3 us, 512 x 14336 15.8 -> 15.3 us; a plain
+// 2-read/1-write stream probe: 82.4% at 256 threads, 84.6% at 128, 84.8% at 64).
 // out may alias gate or up: each element is read and written by the same
 // lane, reads first.
 #include "common.hpp"
@@ -15,7 +18,7 @@
 namespace fence {
 namespace {
 
-constexpr int kSwigluThreads = 256;
+constexpr int kSwigluThreads = 64;
 constexpr int kSwigluUnroll = 1;
 
 // OUT32: fp32 result to `out`; OUT16: its binary16 rounding to `out16`
