@@ -66,7 +66,7 @@ BYTES = {
 STEP_BYTES = sum(BYTES.values())
 SOFTMAX_GENERIC_BYTES = 2 * 4 * SM_HEADS * SM_Q * SM_K
 DOMINANT = "swiglu"
-KERNEL_NAMES = {"softmax": "softmax_vec_kernel", "swiglu": "swiglu_vec_kernel", "rope": "head_ops_vec_kernel"}
+KERNEL_NAMES = {"softmax": "softmax_vec_kernel", "swiglu": "swiglu_vec_kernel", "rope": "head_stream_kernel"}
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "swiglu_config4_pmc.txt")
 
 # Llama-3-8B shapes (configs[1] and the decode-step op set)
@@ -92,6 +92,9 @@ def parse():
                     help="also measure the decode-path ops (GEMVs, attention, epilogues) of every "
                          "config and write the per-op report (JSON) to PATH; a table goes to stderr")
     ap.add_argument("--all-reps", type=int, default=50)
+    ap.add_argument("--all-only", metavar="PATH", default=None,
+                    help="only the device-copy calibration and the --all measurements (written to PATH), "
+                         "no JSON line: the run the per-op rocprofv3 summaries profile")
     return ap.parse_args()
 
 
@@ -310,6 +313,14 @@ def main():
 
     torch.cuda.set_device(0)
     F.lib()
+    if args.all_only:
+        copy_gbps = copy_calibration(torch)
+        res = measure_configs(torch, F, args.all_reps, extended=True)
+        with open(args.all_only, "w") as fh:
+            json.dump({"peak_GBps": PEAK_HBM_GBPS, "reps": args.all_reps, "copy_calibration_GBps": copy_gbps,
+                       "timing": "kernel start/end events (hipExtLaunchKernel)", "results": res}, fh, indent=1)
+        print(f"wrote {args.all_only}: {len(res)} ops", file=sys.stderr)
+        return
     gen = torch.Generator(device="cuda").manual_seed(1234)
     probe = BufferSet(torch, gen)
     set_bytes = sum(t.numel() * t.element_size() for t in vars(probe).values())
@@ -508,7 +519,7 @@ def measure_configs(torch, F, reps, extended):
             lambda: dict(q=randn(32 * 128), k=randn(8 * 128), wq=1 + 0.1 * randn(128), wk=1 + 0.1 * randn(128)),
             lambda b: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), b["wq"].data_ptr(), b["wk"].data_ptr(),
                                      1, 32, 8, 128, 1e-6, None, pos0, 1e6, F.ROPE_NEOX, sh),
-            "head_ops_vec_kernel", note=f"position {pos0}")
+            "head_stream_kernel", note=f"position {pos0}")
     measure(0, "swiglu", "swiglu 9728", 3 * F0 * 4,
             lambda: dict(g=randn(F0), u=randn(F0), o=torch.empty(F0, **dev)),
             lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), F0, sh),
@@ -626,7 +637,7 @@ def measure_configs(torch, F, reps, extended):
                 lambda: dict(q=randn(T2, NQ * HD), k=randn(T2, NKV * HD)),
                 lambda b, style=style: F.qk_norm_rope(b["q"].data_ptr(), b["k"].data_ptr(), wq2.data_ptr(),
                                                       wk2.data_ptr(), T2, NQ, NKV, HD, 1e-6, None, 0, 1e6,
-                                                      style, sh), "head_ops_vec_kernel")
+                                                      style, sh), "head_stream_kernel")
     measure(2, "swiglu", "swiglu 4096x12288", 3 * T2 * F2 * 4,
             lambda: dict(g=randn(T2, F2), u=randn(T2, F2), o=torch.empty(T2, F2, **dev)),
             lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T2 * F2, sh),
