@@ -145,7 +145,8 @@ def test_rms_norm_misaligned(oracle):
     assert_rows_close(host(ob)[1:], oracle.rms_norm(x, w, 1e-6), n, "misaligned rms_norm")
 
 
-@pytest.mark.parametrize("n_heads,hd", [(32, 128), (8, 128), (16, 64), (4, 256), (6, 80), (3, 5)])
+@pytest.mark.parametrize("n_heads,hd", [(32, 128), (8, 128), (2, 128), (5, 128), (16, 64), (4, 256), (6, 80),
+                                         (3, 5)])
 def test_rms_norm_per_head(oracle, n_heads, hd):
     rng = np.random.default_rng(n_heads * hd)
     x, w = normal(rng, (n_heads, hd)), normal(rng, hd, 1.0, 0.1)
@@ -178,16 +179,21 @@ def test_apply_rope_neox(oracle, nq, nkv, hd, base):
     (37, 12, 0, 64, 1e4, NEOX),
     (9, 5, 3, 256, 1e6, INTERLEAVED),
     (9, 5, 3, 48, 1e6, NEOX),               # head_dim not in {64,128,256}: scalar kernel
+    (7, 3, 1, 128, 1e6, NEOX),              # odd head counts: the unit kernel, not the streaming one
+    (9, 6, 0, 128, 1e6, INTERLEAVED),       # q only, streaming kernel
+    (11, 0, 4, 128, 1e6, NEOX),             # k only, streaming kernel
 ])
 def test_rope_rows(oracle, T, nq, nkv, hd, base, style):
     rng = np.random.default_rng(T + nq + hd + style)
     q = normal(rng, (T, nq, hd))
     k = normal(rng, (T, nkv, hd)) if nkv else None
-    dq = dev(q)
+    dq = dev(q) if nq else None
     dk = dev(k) if nkv else None
-    F.rope(dq.data_ptr(), dk.data_ptr() if nkv else None, T, nq, nkv, hd, None, 0, base, style, stream())
+    F.rope(dq.data_ptr() if nq else None, dk.data_ptr() if nkv else None, T, nq, nkv, hd, None, 0, base, style,
+           stream())
     rq, rk = oracle.rope_rows(q, k, None, 0, base, style)
-    assert_rows_close(host(dq), rq, hd, "rope q")
+    if nq:
+        assert_rows_close(host(dq), rq, hd, "rope q")
     if nkv:
         assert_rows_close(host(dk), rk, hd, "rope k")
 
@@ -196,12 +202,13 @@ def test_rope_explicit_positions(oracle):
     rng = np.random.default_rng(77)
     T, nq, nkv, hd = 64, 8, 2, 128
     pos = rng.integers(0, 32768, T).astype(np.int32)
-    q, k = normal(rng, (T, nq, hd)), normal(rng, (T, nkv, hd))
-    dq, dk = dev(q), dev(k)
-    F.rope(dq.data_ptr(), dk.data_ptr(), T, nq, nkv, hd, dev(pos).data_ptr(), 0, 1e6, NEOX, stream())
-    rq, rk = oracle.rope_rows(q, k, pos, 0, 1e6, NEOX)
-    assert_rows_close(host(dq), rq, hd, "rope q positions")
-    assert_rows_close(host(dk), rk, hd, "rope k positions")
+    for style in (NEOX, INTERLEAVED):
+        q, k = normal(rng, (T, nq, hd)), normal(rng, (T, nkv, hd))
+        dq, dk = dev(q), dev(k)
+        F.rope(dq.data_ptr(), dk.data_ptr(), T, nq, nkv, hd, dev(pos).data_ptr(), 0, 1e6, style, stream())
+        rq, rk = oracle.rope_rows(q, k, pos, 0, 1e6, style)
+        assert_rows_close(host(dq), rq, hd, "rope q positions")
+        assert_rows_close(host(dk), rk, hd, "rope k positions")
 
 
 @pytest.mark.parametrize("T,nq,nkv,hd,base,style,pos0", [
@@ -211,17 +218,23 @@ def test_rope_explicit_positions(oracle):
     (33, 16, 4, 64, 1e4, NEOX, 100),
     (5, 4, 4, 256, 1e6, INTERLEAVED, 0),
     (7, 6, 2, 80, 1e6, NEOX, 3),             # scalar kernel
+    (13, 3, 3, 128, 1e6, NEOX, 7),           # odd head counts: the unit kernel
+    (6, 4, 0, 128, 1e6, INTERLEAVED, 1),     # q only, streaming kernel
+    (6, 0, 2, 128, 1e6, NEOX, 4090),         # k only, streaming kernel
 ])
 def test_qk_norm_rope(oracle, T, nq, nkv, hd, base, style, pos0):
     rng = np.random.default_rng(T + hd + style)
     q, k = normal(rng, (T, nq, hd)), normal(rng, (T, nkv, hd))
     wq, wk = normal(rng, hd, 1.0, 0.1), normal(rng, hd, 1.0, 0.1)
-    dq, dk = dev(q), dev(k)
-    F.qk_norm_rope(dq.data_ptr(), dk.data_ptr(), dev(wq).data_ptr(), dev(wk).data_ptr(), T, nq, nkv,
-                   hd, 1e-6, None, pos0, base, style, stream())
+    dq = dev(q) if nq else None
+    dk = dev(k) if nkv else None
+    F.qk_norm_rope(dq.data_ptr() if nq else None, dk.data_ptr() if nkv else None, dev(wq).data_ptr(),
+                   dev(wk).data_ptr(), T, nq, nkv, hd, 1e-6, None, pos0, base, style, stream())
     rq, rk = oracle.qk_norm_rope(q, k, wq, wk, 1e-6, None, pos0, base, style)
-    assert_rows_close(host(dq), rq, hd, "qk_norm_rope q")
-    assert_rows_close(host(dk), rk, hd, "qk_norm_rope k")
+    if nq:
+        assert_rows_close(host(dq), rq, hd, "qk_norm_rope q")
+    if nkv:
+        assert_rows_close(host(dk), rk, hd, "qk_norm_rope k")
 
 
 @pytest.mark.parametrize("T,nq,nkv,hd,eps,base,style,inplace", [
