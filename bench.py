@@ -25,7 +25,9 @@ Also reported from the same run:
     (fence_time_next_launch -> hipExtLaunchKernel, on the launch stream: the
     interval a kernel-trace profiler reports); the roofline of the dominant
     kernel (swiglu) from K such launches;
-  * the same per-op figures for every op of configs[0..3];
+  * the same per-op figures for every op of configs[0..3]; for the configs[1]
+    ops and the one-float4 floor launch also the per-launch time of launches
+    queued back to back, on the stream and replayed from one HIP graph;
   * the Llama-3-8B decode-step op set in microseconds, the Q8_0 LM-head GEMV,
     whole decode steps of a Qwen3-4B-shaped model through the GGUF loader and
     host forward, and a device-copy calibration;
@@ -464,9 +466,67 @@ def measure_configs(torch, F, reps, extended):
 
     scrub = {"buf": None}
 
-    def measure(cfg, key, name, nbytes, make_set, run, kernel, note="", launches=1, warm=False):
+    def back_to_back(sets, run, nbytes):
+        """One event pair around n launches queued back to back (the sets in
+        turn): the per-launch cost when launches follow each other.  A spin
+        kernel holds the stream while the host queues them, so the span is GPU
+        time, not the host's launch rate."""
+        n = max(reps, 2 * len(sets))
+        es, e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        torch.cuda.synchronize()
+        es.record()
+        torch.cuda._sleep(50_000_000)  # the spin: tens of ms, far longer than queueing n launches
+        e0.record()
+        h0 = time.perf_counter()
+        for i in range(n):
+            run(sets[i % len(sets)])
+        queue_ms = (time.perf_counter() - h0) * 1e3
+        e1.record()
+        torch.cuda.synchronize()
+        spin_ms = es.elapsed_time(e0)
+        if queue_ms >= spin_ms:
+            raise RuntimeError(f"back-to-back timing: queueing took {queue_ms:.2f} ms, the spin {spin_ms:.2f} ms")
+        us = e0.elapsed_time(e1) * 1e3 / n
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"us_per_launch": round(us, 3), "GBps": round(gbps, 1), "frac_peak": round(gbps / PEAK_HBM_GBPS, 4),
+                "launches": n, "spin_ms": round(spin_ms, 2), "queue_ms": round(queue_ms, 2)}
+
+    def graph_back_to_back(sets, run, nbytes):
+        """The same n launches captured in one HIP graph, replayed: the
+        per-launch cost without the stream's per-dispatch path (the form a
+        decode or prefill loop replays).  Median of 5 timed replays."""
+        nonlocal sh
+        n = max(reps, 2 * len(sets))
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            saved, sh = sh, cap.cuda_stream  # the ops' lambdas launch on `sh`
+            try:
+                for i in range(n):
+                    run(sets[i % len(sets)])
+            finally:
+                sh = saved
+        g.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / n)
+        del g
+        us = sorted(times)[len(times) // 2]
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"us_per_launch": round(us, 3), "GBps": round(gbps, 1), "frac_peak": round(gbps / PEAK_HBM_GBPS, 4),
+                "launches": n, "replays": len(times)}
+
+    def measure(cfg, key, name, nbytes, make_set, run, kernel, note="", launches=1, warm=False, b2b=False):
         """launches: kernels the call runs; the timing spans the first one's
-        start to the last one's end.  warm: one buffer set, no eviction."""
+        start to the last one's end.  warm: one buffer set, no eviction.
+        b2b: also time launches queued back to back over the same sets."""
         probe = make_set()
         sb = sum(t.numel() * t.element_size() for t in probe.values() if torch.is_tensor(t))
         small = sb < (1 << 20) and not warm
@@ -491,9 +551,16 @@ def measure_configs(torch, F, reps, extended):
                                                     "rotating buffer sets")}
         if note:
             r["note"] = note
+        if b2b:
+            r["back_to_back"] = back_to_back(sets, run, nbytes)
+            r["back_to_back_graph"] = graph_back_to_back(sets, run, nbytes)
         results.append(r)
         print(f"[cfg{cfg}] {name:40s} {r['us_mean']:9.2f} us  {r['GBps']:8.1f} GB/s  "
-              f"{100 * r['frac_peak']:5.1f}%  ({nbytes / 1e6:.2f} MB, {len(sets)} sets)", file=sys.stderr, flush=True)
+              f"{100 * r['frac_peak']:5.1f}%  ({nbytes / 1e6:.2f} MB, {len(sets)} sets)"
+              + (f"  back to back {r['back_to_back']['us_per_launch']:.2f} us "
+                 f"{100 * r['back_to_back']['frac_peak']:.1f}%, in a graph "
+                 f"{r['back_to_back_graph']['us_per_launch']:.2f} us "
+                 f"{100 * r['back_to_back_graph']['frac_peak']:.1f}%" if b2b else ""), file=sys.stderr, flush=True)
         del sets, probe
         torch.cuda.empty_cache()
 
@@ -506,7 +573,7 @@ def measure_configs(torch, F, reps, extended):
     measure("floor", "swiglu_one_float4", "swiglu n=4 (one float4: the per-launch floor)", 48,
             lambda: dict(g=randn(4), u=randn(4), o=torch.empty(4, **dev)),
             lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), 4, sh),
-            "swiglu_vec_kernel", warm=True)
+            "swiglu_vec_kernel", warm=True, b2b=True)
 
     # ---- Qwen3-4B decode, one token, fp32
     E0, F0, V0 = 2560, 9728, 151936
@@ -596,17 +663,17 @@ def measure_configs(torch, F, reps, extended):
             lambda: dict(ids=torch.randint(0, V1, (T1,), dtype=torch.int32, **dev, generator=gen),
                          o=torch.empty(T1, H1, **dev)),
             lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), T1, H1, sh),
-            "q8_gather_kernel")
+            "q8_gather_kernel", b2b=True)
     del tab1
     measure(1, "norm_rope", "rms_norm->rope interleaved Q+K", 2 * T1 * H1 * 4 + H1 * 4 + 2 * T1 * NKV * HD * 4,
             lambda: dict(x=randn(T1, H1), o=torch.empty(T1, H1, **dev), k=randn(T1, NKV * HD)),
             lambda b: F.rms_norm_rope(b["o"].data_ptr(), b["x"].data_ptr(), w1.data_ptr(), b["k"].data_ptr(),
                                       T1, NQ, NKV, HD, 1e-5, None, 0, L3_THETA, F.ROPE_INTERLEAVED, sh),
-            "head_ops_vec_kernel")
+            "head_ops_vec_kernel", b2b=True)
     measure(1, "swiglu", "swiglu 512x14336", 3 * T1 * F1 * 4,
             lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **dev)),
             lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh),
-            "swiglu_vec_kernel")
+            "swiglu_vec_kernel", b2b=True)
     if extended:
         measure(1, "residual_rms_norm_f16", "residual->rms_norm->f16 512x4096", T1 * H1 * (4 + 4 + 4 + 2) + 4 * H1,
                 lambda: dict(h=randn(T1, H1), r=randn(T1, H1), o=torch.empty(T1, H1, **h16)),
