@@ -385,3 +385,29 @@ def test_fuzz_argmax(oracle, seed):
     assert int(host(r)[0]) == want, what + " one workgroup"
     F.argmax_ws(px, r.data_ptr(), n, ws.data_ptr(), ws_bytes, stream())
     assert int(host(r)[0]) == want, what + f" workspace {ws_bytes} B"
+
+
+# ------------------------------------- attention with its q/k prologue fused
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_attention_qk_equals_two_calls(seed):
+    """fence_gqa_attention_qk_f16 (QK-norm, RoPE and the KV store inside the
+    attention launch) against qk_norm_rope_store_kv then gqa_attention_f16:
+    outputs and caches bit for bit."""
+    from test_gpu_decode_fusions import attention_qk_operands, run_attention_qk
+    rng = np.random.default_rng(16000 + seed)
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    nq = nkv * int(rng.choice([1, 2, 3, 4, 5, 8]))
+    hd = int(rng.choice([128, 128, 128, 64]))
+    ctx = int(rng.integers(1, 4200))
+    pos = int(rng.choice([0, ctx - 1, int(rng.integers(0, ctx)), min(ctx - 1, 64 * int(rng.integers(0, 40)))]))
+    norm = bool(rng.integers(0, 4))
+    style = int(rng.choice([NEOX, INTERLEAVED]))
+    ws_floats = int(rng.choice([1, 2, 4])) * nq * ctx + int(rng.integers(0, 200))
+    ops = attention_qk_operands(rng, nq, nkv, hd, ctx, norm)
+    got = run_attention_qk(ops, nq, nkv, hd, pos, 1e6, style, ws_floats, fused=True)
+    ref = run_attention_qk(ops, nq, nkv, hd, pos, 1e6, style, ws_floats, fused=False)
+    what = f"seed {seed}: attention_qk {nq}/{nkv}x{hd} pos {pos} ctx {ctx} norm {norm} style {style} ws {ws_floats}"
+    for g, r, part in zip(got, ref, ("fp32 out", "binary16 out", "k cache", "v cache")):
+        kind = np.uint32 if g.dtype == np.float32 else np.uint16
+        assert np.array_equal(g.view(kind), r.view(kind)), f"{what}: {part}"
