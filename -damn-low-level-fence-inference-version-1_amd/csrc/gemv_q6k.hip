@@ -30,12 +30,14 @@
 // a direct kernel reads the same dwords from global memory.  Rows of more than
 // 16 blocks are split over 2 or 4 waves of the workgroup, whose partial sums
 // meet in LDS.  The lane's x values (16 per pass) stay in VGPRs for all rows.
+// Every kernel adds a row's terms in one order that depends on K alone
+// (q6_wpr, q6_passes), so a row has the same bits in every launch.
 #include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
 
-// How a row's blocks are split over waves (see q6_plan): 0 up to four passes
+// How a row's blocks are split over waves (see q6_wpr): 0 up to four passes
 // (16 blocks) per wave, 1 up to two, 2 one pass where the row allows.
 #ifndef FENCE_GEMV_Q6K_SPLIT
 #define FENCE_GEMV_Q6K_SPLIT 0
@@ -123,6 +125,21 @@ __device__ __forceinline__ void segment(int nb, int seg, int wpr, int* b0, int* 
     *b0 = (nb * seg) / wpr;
     *b1 = (nb * (seg + 1)) / wpr;
 }
+
+// The order a row of nb blocks is summed in, for every kernel: WPR waves (or
+// segments) per row, each over PASSES passes of four blocks; each segment's
+// lane values are added in pass order (a masked block slot adds +0), summed
+// over the wave, and the segment sums added in segment order.  It depends on
+// nb alone, so a row gets the same bits from every launch that contains it:
+// alone or with other matrices, staged or direct.  Rows of more than 64
+// blocks are never staged; the direct kernel gives them one segment.
+__host__ __device__ constexpr int q6_wpr(int nb) {
+    return nb > 4 * kMaxSegBlocks        ? 1
+           : FENCE_GEMV_Q6K_SPLIT == 2 ? (nb <= 4 ? 1 : nb <= 8 ? 2 : 4)
+           : FENCE_GEMV_Q6K_SPLIT == 1 ? (nb <= 8 ? 1 : nb <= 16 ? 2 : 4)
+                                       : (nb <= 16 ? 1 : nb <= 32 ? 2 : 4);
+}
+__host__ __device__ constexpr int q6_passes(int nb) { return (nb + 4 * q6_wpr(nb) - 1) / (4 * q6_wpr(nb)); }
 
 template <int PASSES>
 __device__ __forceinline__ void load_x(uint32_t (&xh)[PASSES][8], float (&kb)[PASSES][4], const uint16_t* x16,
@@ -505,44 +522,56 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
     for (; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::false_type{});
 }
 
-// y . row lr of Wm, summed over the wave (lane 0 holds it): the direct
-// kernel's dwords come straight from global memory, two aligned dwords each,
+// The lane's value of block b of row lr (its 16 weights), for the direct
+// kernel: dwords straight from global memory, two aligned dwords each,
 // realigned.
+__device__ __forceinline__ float direct_block(const uint8_t* Wm, const uint16_t* x16, int64_t lr, int nb, int b,
+                                              int h, int j) {
+    const uint8_t* blk = Wm + lr * static_cast<int64_t>(nb) * kBlockBytes + static_cast<int64_t>(b) * kBlockBytes;
+    auto rd = [&](int off) {
+        const uint8_t* p = blk + off;
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+        const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3);
+        // both dwords lie inside the 210-byte block for every offset used
+        return sh ? __builtin_amdgcn_alignbyte(w[1], w[0], sh) : w[0];
+    };
+    const uint32_t a = rd(64 * h + 4 * j), bq = rd(64 * h + 32 + 4 * j), c = rd(128 + 32 * h + 4 * j);
+    int sc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sc[q] = static_cast<int8_t>(blk[192 + 8 * h + (j >> 2) + 2 * q]);
+    const uint16_t dbits = static_cast<uint16_t>(blk[208] | (blk[209] << 8));
+    uint32_t xh[8];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        const int e = 256 * b + 128 * h + 32 * cc + 4 * j;
+        xh[2 * cc] = x16[e] | (static_cast<uint32_t>(x16[e + 1]) << 16);
+        xh[2 * cc + 1] = x16[e + 2] | (static_cast<uint32_t>(x16[e + 3]) << 16);
+    }
+    float kbc[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) kbc[cc] = q6_col_bias(xh[2 * cc], xh[2 * cc + 1]);
+    const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+    return q6_lane_dot(q6_unpack(a, bq, c), xh, kbc, sc, d);
+}
+
+// y . row lr of Wm (lane 0 holds it), summed in the order of q6_wpr /
+// q6_passes -- the staged kernel's -- one segment after another.
 __device__ __forceinline__ float direct_row(const uint8_t* Wm, const uint16_t* x16, int64_t lr, int nb, int lane) {
     const int bslot = lane >> 4, h = (lane >> 3) & 1, j = lane & 7;
-    const int64_t row_bytes = static_cast<int64_t>(nb) * kBlockBytes;
-    float part = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += 4) {
-        const int b = b0 + bslot;
-        if (b < nb) {
-            const uint8_t* blk = Wm + lr * row_bytes + static_cast<int64_t>(b) * kBlockBytes;
-            auto rd = [&](int off) {
-                const uint8_t* p = blk + off;
-                const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
-                const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3);
-                // both dwords lie inside the 210-byte block for every offset used
-                return sh ? __builtin_amdgcn_alignbyte(w[1], w[0], sh) : w[0];
-            };
-            const uint32_t a = rd(64 * h + 4 * j), bq = rd(64 * h + 32 + 4 * j), c = rd(128 + 32 * h + 4 * j);
-            int sc[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) sc[q] = static_cast<int8_t>(blk[192 + 8 * h + (j >> 2) + 2 * q]);
-            const uint16_t dbits = static_cast<uint16_t>(blk[208] | (blk[209] << 8));
-            uint32_t xh[8];
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                const int e = 256 * b + 128 * h + 32 * cc + 4 * j;
-                xh[2 * cc] = x16[e] | (static_cast<uint32_t>(x16[e + 1]) << 16);
-                xh[2 * cc + 1] = x16[e + 2] | (static_cast<uint32_t>(x16[e + 3]) << 16);
-            }
-            float kbc[4];
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) kbc[cc] = q6_col_bias(xh[2 * cc], xh[2 * cc + 1]);
-            const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
-            part += q6_lane_dot(q6_unpack(a, bq, c), xh, kbc, sc, d);
+    const int wpr = q6_wpr(nb), passes = q6_passes(nb);
+    float total = 0.0f;
+    for (int seg = 0; seg < wpr; ++seg) {
+        int b0, b1;
+        segment(nb, seg, wpr, &b0, &b1);
+        float part = 0.0f;
+        for (int p = 0; p < passes; ++p) {
+            const int b = b0 + 4 * p + bslot;
+            part += b < b1 ? direct_block(Wm, x16, lr, nb, b, h, j) : 0.0f;  // a masked slot adds +0
         }
+        part = wave_sum(part);
+        total = seg == 0 ? part : total + part;
     }
-    return wave_sum(part);
+    return total;
 }
 
 // Direct kernel for any alignment and any K: one wave per row (PAIR: per
@@ -608,35 +637,28 @@ int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, co
                        (n_out + out_per_group - 1) / out_per_group, s, job, x, nb, rin);
 }
 
-// (PASSES, WPR) of a row of nb blocks: WPR waves per row, each over at most
-// 4 * PASSES blocks.  It depends on nb alone, so every matrix of a multi or
-// pair launch sums its rows in the same order as its own launch would.
-// NORM launches take rows of up to 32 blocks.
+// The staged kernel for a row of nb blocks, at q6_wpr / q6_passes.  Only the
+// (PASSES, WPR) pairs the compiled split table produces are instantiated; NORM
+// launches take rows of up to 32 blocks.
 template <bool PAIR, bool MULTI, int NORM>
 int launch_nb(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
+    const int w = q6_wpr(nb), p = q6_passes(nb);
+    if (nb > 4 * kMaxSegBlocks || (NORM != 0 && nb > 32)) return FENCE_ERROR_INVALID_VALUE;  // callers check nb
+#define FENCE_Q6_STAGED(P, W)                                                   \
+    if (p == P && w == W) return launch_staged<P, W, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
     if constexpr (FENCE_GEMV_Q6K_SPLIT == 2) {
-        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 8) return launch_staged<1, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 16) return launch_staged<1, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        FENCE_Q6_STAGED(1, 1) FENCE_Q6_STAGED(1, 2) FENCE_Q6_STAGED(1, 4) FENCE_Q6_STAGED(2, 4)
     } else if constexpr (FENCE_GEMV_Q6K_SPLIT == 1) {
-        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 16) return launch_staged<2, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        FENCE_Q6_STAGED(1, 1) FENCE_Q6_STAGED(2, 1) FENCE_Q6_STAGED(2, 2) FENCE_Q6_STAGED(2, 4)
     } else {
-        if (nb <= 4) return launch_staged<1, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 8) return launch_staged<2, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 12) return launch_staged<3, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 16) return launch_staged<4, 1, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 24) return launch_staged<3, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        if (nb <= 32) return launch_staged<4, 2, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+        FENCE_Q6_STAGED(1, 1) FENCE_Q6_STAGED(2, 1) FENCE_Q6_STAGED(3, 1) FENCE_Q6_STAGED(4, 1)
+        FENCE_Q6_STAGED(3, 2) FENCE_Q6_STAGED(4, 2)
     }
-    if (nb <= 32) return launch_staged<2, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-    if constexpr (NORM != 0) {
-        return FENCE_ERROR_INVALID_VALUE;  // not dispatched: the caller checks nb
-    } else {
-        if (nb <= 48) return launch_staged<3, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
-        return launch_staged<4, 4, PAIR, MULTI, NORM>(job, n_out, x, nb, rin, s);
+    if constexpr (NORM == 0) {
+        FENCE_Q6_STAGED(3, 4) FENCE_Q6_STAGED(4, 4)
     }
+#undef FENCE_Q6_STAGED
+    return FENCE_ERROR_INVALID_VALUE;  // a pair the table cannot produce
 }
 
 template <bool PAIR>

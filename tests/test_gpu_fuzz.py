@@ -411,3 +411,73 @@ def test_fuzz_attention_qk_equals_two_calls(seed):
     for g, r, part in zip(got, ref, ("fp32 out", "binary16 out", "k cache", "v cache")):
         kind = np.uint32 if g.dtype == np.float32 else np.uint16
         assert np.array_equal(g.view(kind), r.view(kind)), f"{what}: {part}"
+
+
+# ------------------------------------------- Q6_K launches of several matrices
+
+def q6k_shape(rng, max_blocks=40, budget=6_000_000):
+    K = 256 * int(rng.integers(1, max_blocks + 1))
+    return K, max(1, budget // K)
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_gemv_q6k_multi_equals_separate_launches(seed):
+    import test_gpu_q6k as q6
+    rng = np.random.default_rng(17000 + seed)
+    K, cap = q6k_shape(rng)
+    n = int(rng.integers(1, 5))
+    Ms = [int(rng.integers(0, min(3000, cap // n) + 1)) for _ in range(n)]
+    if not any(Ms):
+        Ms[0] = 1
+    Ws = [make_q6k_matrix(rng, M, K) if M else np.zeros((0, K // 256 * 210), np.uint8) for M in Ms]
+    x = q6.rand_x(rng, K)
+    got = q6.run_q6k_multi([W if W.size else None for W in Ws], x, Ms, K)
+    for i, (W, M) in enumerate(zip(Ws, Ms)):
+        if M:
+            assert np.array_equal(got[i].view(np.uint32), q6.run_q6k(W, x, M, K).view(np.uint32)), \
+                f"seed {seed}: multi {Ms} K={K}: matrix {i} differs from its own launch"
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_gemv_q6k_swiglu_equals_unfused(seed):
+    import test_gpu_q6k as q6
+    rng = np.random.default_rng(18000 + seed)
+    K, cap = q6k_shape(rng)
+    M = int(rng.integers(1, min(6000, cap // 2) + 1))
+    Wg, Wu = make_q6k_matrix(rng, M, K), make_q6k_matrix(rng, M, K)
+    x = q6.rand_x(rng, K, std=0.5)
+    got16, got32 = q6.run_swiglu(Wg, Wu, x, M, K)
+    ref16, ref32 = q6.unfused_swiglu(Wg, Wu, x, M, K)
+    what = f"seed {seed}: gate/up pair {M}x{K}"
+    assert np.array_equal(got32.view(np.uint32), ref32.view(np.uint32)), what + ": fp32 act"
+    assert np.array_equal(got16, ref16), what + ": binary16 act"
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_gemv_q6k_rms_prologue_equals_norm_then_gemv(seed):
+    """The GEMVs that compute their own layer-boundary input row: bit for bit
+    the norm launch followed by the plain GEMV (multi and gate/up pair)."""
+    import test_gpu_gemv_rms as gr
+    rng = np.random.default_rng(19000 + seed)
+    K, cap = q6k_shape(rng, max_blocks=36)
+    residual = bool(rng.integers(0, 4))
+    hid, res, w = gr.row(rng, K, residual)
+    if rng.integers(0, 2):
+        n = int(rng.integers(1, 4))
+        Ms = [int(rng.integers(0, min(2500, cap // n) + 1)) for _ in range(n)]
+        if not any(Ms):
+            Ms[0] = 1
+        Ws = [make_q6k_matrix(rng, M, K) if M else np.zeros((0, K // 256 * 210), np.uint8) for M in Ms]
+        gr.check_multi(Ws, Ms, K, hid, res, w, hid_off=int(rng.choice([0, 0, 0, 1])))
+        return
+    M = int(rng.integers(1, min(5000, cap // 2) + 1))
+    Wg, Wu = make_q6k_matrix(rng, M, K), make_q6k_matrix(rng, M, K)
+    got16, got32, hout, x16 = gr.run_pair(Wg, Wu, M, K, hid, res, w)
+    ref_h, ref_x = gr.unfused_input(hid, res, w, K)
+    what = f"seed {seed}: pair with norm {M}x{K} residual {residual}"
+    assert np.array_equal(x16, ref_x), what + ": x"
+    if residual:
+        assert np.array_equal(hout.view(np.uint32), ref_h.view(np.uint32)), what + ": hidden_out"
+    ref16, ref32 = __import__("test_gpu_q6k").run_swiglu(Wg, Wu, ref_x, M, K)
+    assert np.array_equal(got16, ref16), what + ": binary16 act"
+    assert np.array_equal(got32.view(np.uint32), ref32.view(np.uint32)), what + ": fp32 act"

@@ -132,6 +132,40 @@ def test_gemv_q6k_bias(oracle):
     assert_close(got, ref, abs_scale(W, x, K), "q6k bias", slack=2.0 ** -23 * np.abs(ref))
 
 
+@pytest.mark.parametrize("nb", [13, 16, 17, 21, 24, 27, 32, 33, 40, 48, 49, 60, 64, 65, 70])
+def test_direct_kernel_sums_in_the_staged_order(nb):
+    """The direct kernel (weights only 2-byte aligned) must give every row the
+    staged kernel's bits: rows of more than 16 blocks are summed per segment
+    of 2 or 4 waves there, so the direct kernel sums in the same segments."""
+    torch = torch_mod()
+    K, M = 256 * nb, 64
+    rng = np.random.default_rng(nb)
+    W = make_q6k_matrix(rng, M, K)
+    x = rand_x(rng, K)
+    staged = run_q6k(W, x, M, K)
+    raw = torch.zeros(W.size + 16, dtype=torch.uint8, device="cuda")
+    raw[2:2 + W.size] = dev(W.reshape(-1))
+    y = torch.full((M,), float("nan"), dtype=torch.float32, device="cuda")
+    LIVE.extend([raw, y])
+    F.gemv_q6k(raw.data_ptr() + 2, dev(x.view(np.int16)).data_ptr(), y.data_ptr(), M, K, stream())
+    assert np.array_equal(host(y).view(np.uint32), staged.view(np.uint32)), "direct differs from staged"
+
+
+@pytest.mark.parametrize("shapes,K", [((176, 73, 25, 103), 6912), ((248, 5), 5376), ((80, 139, 79), 9984),
+                                      ((59, 43, 76, 99), 9728)])
+def test_multi_with_a_matrix_that_cannot_be_staged(oracle, shapes, K):
+    """One matrix of the launch has M * nb not a multiple of 8, so the whole
+    launch runs the direct kernel while the others, alone, are staged: each
+    must still equal its own launch bit for bit."""
+    rng = np.random.default_rng(sum(shapes) + K)
+    Ws = [make_q6k_matrix(rng, M, K) for M in shapes]
+    x = rand_x(rng, K)
+    got = run_q6k_multi(Ws, x, list(shapes), K)
+    for i, (W, M) in enumerate(zip(Ws, shapes)):
+        assert np.array_equal(got[i].view(np.uint32), run_q6k(W, x, M, K).view(np.uint32)), f"matrix {i}"
+        assert_close(got[i], oracle.gemv_q6k(W, x), abs_scale(W, x, K), f"multi {i}")
+
+
 def test_gemv_q6k_unaligned_operands(oracle):
     """W only 2-byte aligned (direct kernel) and x 2-byte aligned."""
     torch = torch_mod()
