@@ -481,3 +481,73 @@ def test_fuzz_gemv_q6k_rms_prologue_equals_norm_then_gemv(seed):
     ref16, ref32 = __import__("test_gpu_q6k").run_swiglu(Wg, Wu, ref_x, M, K)
     assert np.array_equal(got16, ref16), what + ": binary16 act"
     assert np.array_equal(got32.view(np.uint32), ref32.view(np.uint32)), what + ": fp32 act"
+
+
+# ------------------------------- QK-norm -> RoPE -> KV store, and attention_f16
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_qk_norm_rope_store_kv_equals_separate_calls(seed):
+    """The fused prologue of a decode step against qk_norm_rope (or rope)
+    then one store_kv per token: q, k and both caches bit for bit, with
+    device positions (distinct, in range) or consecutive ones from pos0."""
+    import test_gpu_decode_fusions as df
+    rng = np.random.default_rng(20000 + seed)
+    T = int(rng.integers(1, 9))
+    hd = int(rng.choice([64, 96, 128, 128, 128, 256]))
+    nkv = int(rng.integers(1, 9))
+    nq = nkv * int(rng.integers(1, 6))
+    ctx = int(rng.integers(T, 5000))
+    norm = bool(rng.integers(0, 4))
+    style = int(rng.choice([NEOX, INTERLEAVED]))
+    positions = rng.choice(ctx, T, replace=False).astype(np.int32) if rng.integers(0, 2) else None
+    pos0 = int(rng.integers(0, ctx - T + 1))
+    q = rng.standard_normal((T, nq, hd)).astype(np.float32)
+    k = rng.standard_normal((T, nkv, hd)).astype(np.float32)
+    v = rng.standard_normal((T, nkv, hd)).astype(np.float32)
+    wq = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+    wk = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+    kc, vc = df.caches(rng, ctx, nkv * hd)
+    got = df.run_fused_kv(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, pos0, 1e6, style)
+    ref = df.run_separate(q, k, v, wq, wk, kc, vc, T, nq, nkv, hd, positions, pos0, 1e6, style)
+    what = (f"seed {seed}: qk_norm_rope_store_kv T={T} {nq}/{nkv}x{hd} ctx {ctx} norm {norm} style {style} "
+            f"positions {positions is not None}")
+    for g, r, part in zip(got, ref, ("q", "k", "k cache", "v cache")):
+        kind = np.uint32 if g.dtype == np.float32 else np.uint16
+        assert np.array_equal(g.view(kind), r.view(kind)), f"{what}: {part}"
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_attention_f16_equals_attention_then_conversion(seed):
+    torch = torch_mod()
+    rng = np.random.default_rng(21000 + seed)
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    n_q = nkv * int(rng.choice([1, 2, 3, 4, 8]))
+    hd = int(rng.choice([64, 96, 128, 128, 128]))
+    ctx = int(rng.integers(1, 4200))
+    seq = int(rng.integers(1, ctx + 1))
+    ws_floats = int(rng.choice([1, 2, 4])) * n_q * ctx
+    kc = rng.standard_normal((ctx, nkv * hd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((ctx, nkv * hd)).astype(np.float16).view(np.uint16)
+    q = (rng.standard_normal(n_q * hd) * 0.3).astype(np.float32)
+    qd, kd, vd = dev(q), dev(kc.view(np.int16)), dev(vc.view(np.int16))
+    ws = torch.empty(ws_floats, dtype=torch.float32, device="cuda")
+    ref32 = torch.empty(n_q * hd, dtype=torch.float32, device="cuda")
+    ref16 = torch.empty(n_q * hd, dtype=torch.int16, device="cuda")
+    got32 = torch.full((n_q * hd,), float("nan"), dtype=torch.float32, device="cuda")
+    got16 = torch.full((n_q * hd,), -1, dtype=torch.int16, device="cuda")
+    LIVE.extend([ws, ref32, ref16, got32, got16])
+    both16 = torch.full((n_q * hd,), -1, dtype=torch.int16, device="cuda")
+    LIVE.append(both16)
+    # fp32 and binary16 from one call; binary16 alone from another
+    F.gqa_attention_f16(got32.data_ptr(), both16.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), hd, n_q,
+                        nkv, seq, ctx, ws.data_ptr(), ws_floats, stream())
+    F.f32_to_f16(ref16.data_ptr(), got32.data_ptr(), n_q * hd, stream())
+    F.gqa_attention_f16(None, got16.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), hd, n_q, nkv, seq, ctx,
+                        ws.data_ptr(), ws_floats, stream())
+    what = f"seed {seed}: attention_f16 {n_q}/{nkv}x{hd} seq {seq} ctx {ctx} ws {ws_floats}"
+    assert np.array_equal(host(both16), host(ref16)), what + ": binary16 != RNE(own fp32)"
+    assert np.array_equal(host(got16), host(ref16)), what + ": binary16-only call differs"
+    if ws_floats == n_q * ctx:  # the reference's score_buf size: the plain entry point splits the same way
+        F.gqa_attention(ref32.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), hd, n_q, nkv, seq, ctx,
+                        ws.data_ptr(), stream())
+        assert np.array_equal(host(got32).view(np.uint32), host(ref32).view(np.uint32)), what + ": fp32"
