@@ -238,10 +238,16 @@ constexpr int staged_waves() { return NORM && !PAIR && WPR == 1 ? 8 : (PAIR && W
 // to LDS, where the row's first wave adds each lane's four in pass order
 // before the wave sum: the additions of one wave doing four passes, so the
 // rows are bit-identical to <4, 1>'s, computed by WPR times as many waves.
+// XW launches also load each wave's next row group while the current one is
+// computed (one chunk slot per lane: 4 VGPRs).  Measured on MI355X, p50 of
+// 400, in-process A/B: the o projection 2560 x 4096 4.92 -> 4.60 us, Llama-3-8B
+// 4096 x 4096 6.44 -> 5.80 us; the same prefetch in the other layouts cost
+// more registers than it saved (gate/up pair, 9728 x 2560) or changed nothing.
 template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
     static_assert(!XW || (PASSES * WPR == 4 && !PAIR && NORM == 0), "XW: four passes, plain rows");
+    constexpr bool PF = XW;  // prefetch the next row group
     constexpr int NW = staged_waves<WPR, PAIR, NORM>();
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
@@ -438,6 +444,18 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
                 const uint32_t dst = cc < nch ? 16u * cc : static_cast<uint32_t>(kBufBytes - 16);
                 *reinterpret_cast<u4*>(buf + dst) = ch[k];
             }
+            if constexpr (PF) {  // the next group's chunks, in flight during this group's dot products
+                const int64_t gn = g + gridDim.x;
+                if (gn * kOutPerGroup < n_out) {  // workgroup-uniform
+                    int64_t on, lrn, an;
+                    int mn, ncn;
+                    uint32_t dn;
+                    row_of(gn, &on, &mn, &lrn);
+                    seg_of(lrn, &an, &ncn, &dn);
+                    load_seg(job.W[mn], an, ncn, ch);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
         }
         if (valid) {
             // The lane's block starts at `base` in the buffer for pass 0 and
@@ -514,12 +532,22 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
             __syncthreads();  // red[] is rewritten by the next group
         }
     };
-    int64_t g = blockIdx.x;
-    if constexpr (NORM != 0) {
-        run_group(g, std::true_type{});  // g < the group count: the grid is at most that
-        g += gridDim.x;
+    if constexpr (PF) {  // the first group's chunks here, every later one's a group ahead
+        int64_t o, lr, a0;
+        int m, nch;
+        uint32_t delta;
+        row_of(blockIdx.x, &o, &m, &lr);
+        seg_of(lr, &a0, &nch, &delta);
+        load_seg(job.W[m], a0, nch, ch);
+        for (int64_t g = blockIdx.x; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::true_type{});
+    } else {
+        int64_t g = blockIdx.x;
+        if constexpr (NORM != 0) {
+            run_group(g, std::true_type{});  // g < the group count: the grid is at most that
+            g += gridDim.x;
+        }
+        for (; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::false_type{});
     }
-    for (; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::false_type{});
 }
 
 // The lane's value of block b of row lr (its 16 weights), for the direct
