@@ -85,7 +85,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--config-reps", type=int, default=20,
                     help="launches per op of configs[0..3] (0 skips them)")
-    ap.add_argument("--decode-reps", type=int, default=300)
+    ap.add_argument("--decode-reps", type=int, default=1000)
     ap.add_argument("--decode-tokens", type=int, default=32,
                     help="tokens of the Qwen3-4B-shaped decode run (0 skips it)")
     ap.add_argument("--lm-head-reps", type=int, default=60,
@@ -890,8 +890,23 @@ def decode_op_set(torch, F, gen, reps):
     us = sorted(a.elapsed_time(b) * 1e3 for a, b in ts)
     out = {"us_p50": round(us[len(us) // 2], 2), "us_p10": round(us[len(us) // 10], 2),
            "us_p90": round(us[(9 * len(us)) // 10], 2), "pos": pos, "launches": 6, "target_us": 60,
-           "measure": "one event pair around each op set (p50 over reps); sustained = reps back to back "
+           "reps": reps,
+           "measure": "one event pair around each op set (p50 over reps; includes any wait for the host's "
+                      "launches); queued = the same with a spin kernel ahead of each op set, so its six launches "
+                      "are queued before the first starts (GPU time only); sustained = reps back to back "
                       "between one event pair"}
+    qs = []
+    for _ in range(reps):
+        torch.cuda._sleep(500_000)  # ~0.2 ms: longer than queueing six launches
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        step()
+        e1.record(s)
+        qs.append((e0, e1))
+    torch.cuda.synchronize()
+    qus = sorted(a.elapsed_time(b) * 1e3 for a, b in qs)
+    out.update({"queued_us_p50": round(qus[len(qus) // 2], 2), "queued_us_p10": round(qus[len(qus) // 10], 2),
+                "queued_us_p90": round(qus[(9 * len(qus)) // 10], 2)})
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
     for _ in range(reps):
