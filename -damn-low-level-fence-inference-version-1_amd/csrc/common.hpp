@@ -276,6 +276,10 @@ inline bool rms_row_plan(int64_t rows, int n, unsigned* threads, int* vpt) {
 int residual_rms_f16_launch(float* hid_out, uint16_t* x16, const float* hid, const float* res, const float* w,
                             int n, float eps, hipStream_t s);
 
+// Lanes one launch of a one-pass kernel may cover.  A dispatch's grid size in
+// lanes is a 32-bit field, so arrays beyond this take several launches.
+constexpr int64_t kMaxLaunchLanes = int64_t(1) << 30;
+
 inline unsigned grid_1d(int64_t units, int64_t per_block, int64_t cap = 1 << 30) {
     int64_t g = (units + per_block - 1) / per_block;
     if (g < 1) g = 1;

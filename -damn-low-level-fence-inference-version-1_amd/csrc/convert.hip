@@ -58,10 +58,12 @@ int convert_launch(void* dst, const void* src, int64_t n, hipStream_t s) {
     int64_t done = 0;
     if (aligned(dst, 4 * dst_size) && aligned(src, 4 * src_size)) {
         const int64_t n4 = n / 4;
-        if (n4 > 0) {
-            const unsigned grid = grid_1d(n4, kThreads, int64_t(1) << 31);
-            if (static_cast<int64_t>(grid) * kThreads < n4) return FENCE_ERROR_INVALID_VALUE;
-            if (int st = launch(convert_vec_kernel<OP>, dim3(grid), dim3(kThreads), 0, s, dst, src, n4)) return st;
+        for (int64_t c0 = 0; c0 < n4; c0 += kMaxLaunchLanes) {  // one launch per kMaxLaunchLanes float4s
+            const int64_t m4 = n4 - c0 < kMaxLaunchLanes ? n4 - c0 : kMaxLaunchLanes;
+            void* d = static_cast<uint8_t*>(dst) + 4 * dst_size * c0;
+            const void* sp = static_cast<const uint8_t*>(src) + 4 * src_size * c0;
+            if (int st = launch(convert_vec_kernel<OP>, dim3(grid_1d(m4, kThreads)), dim3(kThreads), 0, s, d, sp, m4))
+                return st;
         }
         done = n4 * 4;
     }

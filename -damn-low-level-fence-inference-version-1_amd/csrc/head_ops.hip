@@ -403,7 +403,7 @@ int dispatch(bool vec, int G, unsigned grid, unsigned threads, hipStream_t s, co
     if (!vec) return launch(head_ops_scalar_kernel<ROPE, NORM>, dim3(grid), dim3(256), 0, s, a, hd, tab);
     if constexpr (NORM != kNormRow) {
         if (G == 16 && !a.kc && a.nq % 2 == 0 && a.nkv % 2 == 0 &&
-            a.tokens * (a.nq + a.nkv) / 2 < (int64_t(1) << 31))
+            a.tokens * (a.nq + a.nkv) / 2 * 64 <= kMaxLaunchLanes)  // else the grid-strided unit kernel
             return launch_stream<ROPE, NORM>(a, tab, s);
     }
     if constexpr (ROPE != kRopeNone && NORM != kNormRow) {  // the KV store follows a RoPE

@@ -82,14 +82,19 @@ int swiglu_launch(float* out, uint16_t* out16, const float* gate, const float* u
     int64_t done = 0;
     if (vec) {
         const int64_t n4 = n / 4;
-        if (n4 > 0) {
-            const unsigned grid = grid_1d(n4, kSwigluThreads * kSwigluUnroll, int64_t(1) << 31);
-            if (static_cast<int64_t>(grid) * kSwigluThreads * kSwigluUnroll < n4)
-                return FENCE_ERROR_INVALID_VALUE;  // beyond 2^31 workgroups
+        // one launch per kMaxLaunchLanes lanes (each lane kSwigluUnroll float4s)
+        constexpr int64_t kChunk4 = kMaxLaunchLanes * kSwigluUnroll;
+        for (int64_t c0 = 0; c0 < n4; c0 += kChunk4) {
+            const int64_t m4 = n4 - c0 < kChunk4 ? n4 - c0 : kChunk4;
+            const unsigned grid = grid_1d(m4, kSwigluThreads * kSwigluUnroll);
+            float* o = out ? out + 4 * c0 : nullptr;
+            uint16_t* o16 = out16 ? out16 + 4 * c0 : nullptr;
+            const float* g = gate + 4 * c0;
+            const float* u = up + 4 * c0;
             int st;
-            if (out && !out16) st = launch_swiglu_vec<true, false>(grid, s, out, out16, gate, up, n4);
-            else if (!out) st = launch_swiglu_vec<false, true>(grid, s, out, out16, gate, up, n4);
-            else st = launch_swiglu_vec<true, true>(grid, s, out, out16, gate, up, n4);
+            if (out && !out16) st = launch_swiglu_vec<true, false>(grid, s, o, o16, g, u, m4);
+            else if (!out) st = launch_swiglu_vec<false, true>(grid, s, o, o16, g, u, m4);
+            else st = launch_swiglu_vec<true, true>(grid, s, o, o16, g, u, m4);
             if (st) return st;
         }
         done = n4 * 4;
