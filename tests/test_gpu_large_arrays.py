@@ -23,6 +23,7 @@ def windows(n):
 
 
 def _free_gib(torch):
+    torch.cuda.empty_cache()  # blocks the caching allocator still holds from earlier tests
     free, _ = torch.cuda.mem_get_info()
     return free / 2**30
 
