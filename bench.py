@@ -556,17 +556,17 @@ def measure_configs(torch, F, reps, extended, back_to_back_timing=True):
             r["note"] = note
         if b2b and back_to_back_timing:
             # extra views of the same op: a failure here is reported, not fatal to the run
-            for key, how in (("back_to_back", back_to_back), ("back_to_back_graph", graph_back_to_back)):
+            for view, how in (("back_to_back", back_to_back), ("back_to_back_graph", graph_back_to_back)):
                 try:
-                    r[key] = how(sets, run, nbytes)
+                    r[view] = how(sets, run, nbytes)
                 except Exception as exc:  # noqa: BLE001
                     torch.cuda.synchronize()
-                    r[key] = {"error": str(exc)[:200]}
+                    r[view] = {"error": str(exc)[:200]}
         results.append(r)
         extra = ""
-        for key, label in (("back_to_back", "back to back"), ("back_to_back_graph", "in a graph")):
-            if "us_per_launch" in r.get(key, {}):
-                extra += f"  {label} {r[key]['us_per_launch']:.2f} us {100 * r[key]['frac_peak']:.1f}%"
+        for view, label in (("back_to_back", "back to back"), ("back_to_back_graph", "in a graph")):
+            if "us_per_launch" in r.get(view, {}):
+                extra += f"  {label} {r[view]['us_per_launch']:.2f} us {100 * r[view]['frac_peak']:.1f}%"
         print(f"[cfg{cfg}] {name:40s} {r['us_mean']:9.2f} us  {r['GBps']:8.1f} GB/s  "
               f"{100 * r['frac_peak']:5.1f}%  ({nbytes / 1e6:.2f} MB, {len(sets)} sets)" + extra,
               file=sys.stderr, flush=True)
