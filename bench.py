@@ -395,17 +395,30 @@ def main():
                           "pass after the timed region, same cold buffer rotation",
                 "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT)}
 
-    configs = {}
-    if args.config_reps > 0:
-        for r in measure_configs(torch, F, args.config_reps, extended=False):
-            configs.setdefault(str(r.pop("config")), {})[r.pop("key")] = r
-    decode = decode_op_set(torch, F, gen, args.decode_reps)
-    lm_head = lm_head_gemv(torch, F, gen, args.lm_head_reps)
-    decode_model = decode_qwen3_4b(torch, args.decode_tokens)
-    copy_gbps = copy_calibration(torch)
+    def section(name, fn):
+        """The sections after the headline: a failure is reported in the line
+        (and on stderr) instead of costing the measurement above."""
+        try:
+            return fn()
+        except Exception as exc:  # noqa: BLE001
+            print(f"bench: {name} failed: {exc}", file=sys.stderr, flush=True)
+            return {"error": str(exc)[:300]}
 
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
-    cpu_all = None if args.no_cpu else cpu_baseline_all_cores(args.cpu_seconds / 2)
+    def config_ops():
+        configs = {}
+        if args.config_reps > 0:
+            for r in measure_configs(torch, F, args.config_reps, extended=False):
+                configs.setdefault(str(r.pop("config")), {})[r.pop("key")] = r
+        return configs
+    configs = section("configs", config_ops)
+    decode = section("decode_op_set", lambda: decode_op_set(torch, F, gen, args.decode_reps))
+    lm_head = section("lm_head_gemv", lambda: lm_head_gemv(torch, F, gen, args.lm_head_reps))
+    decode_model = section("decode_qwen3_4b", lambda: decode_qwen3_4b(torch, args.decode_tokens))
+    copy_gbps = section("copy_calibration", lambda: copy_calibration(torch))
+
+    cpu = None if args.no_cpu else section("cpu_baseline", lambda: cpu_baseline(args.cpu_seconds))
+    cpu_all = None if args.no_cpu else section("cpu_baseline_all_cores",
+                                               lambda: cpu_baseline_all_cores(args.cpu_seconds / 2))
     if args.all:
         res = measure_configs(torch, F, args.all_reps, extended=True)
         with open(args.all, "w") as fh:
