@@ -107,16 +107,18 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int* __restrict__ result, 
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             if (bi[c] >= 0) key = umax64(key, argmax_key(bv[c], bi[c]));
-        const int tail = 4 * n4 + t;  // the last n % 4 elements, one per lane
+        // the last n % 4 elements, one per lane; in 64 bits, since 4 * n4 + t
+        // passes INT_MAX when n is within one grid of it
+        const int64_t tail = 4 * static_cast<int64_t>(n4) + t;
         if (tail < n) {
             const float v = x[tail];
-            if (v > kArgmaxInit) key = umax64(key, argmax_key(v, tail));
+            if (v > kArgmaxInit) key = umax64(key, argmax_key(v, static_cast<int>(tail)));
         }
     } else {
         float bv = kArgmaxInit;
         int bi = -1;
-        for (int i = t; i < n; i += stride)
-            if (x[i] > bv) bv = x[i], bi = i;
+        for (int64_t i = t; i < n; i += stride)  // 64-bit: i + stride may pass INT_MAX
+            if (x[i] > bv) bv = x[i], bi = static_cast<int>(i);
         if (bi >= 0) key = argmax_key(bv, bi);
     }
     key = block_max_key(key);
@@ -191,11 +193,19 @@ uint64_t* g_scratch_ptr[kMaxDevices] = {};
 std::mutex g_scratch_mu;
 
 // This device's address of `scratch`, looked up on the device's first call.
-int scratch_ptr(uint64_t** out) {
+// The stream must belong to the current device (the address is that
+// device's); a stream of another device is rejected.
+int scratch_ptr(hipStream_t s, uint64_t** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e);
     if (dev < 0 || dev >= kMaxDevices) return FENCE_ERROR_INVALID_VALUE;
+    if (s) {
+        int sdev = -1;
+        e = hipStreamGetDevice(s, &sdev);
+        if (e != hipSuccess) return hip_status(e);
+        if (sdev != dev) return FENCE_ERROR_INVALID_VALUE;
+    }
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
         void* p = nullptr;
@@ -213,7 +223,7 @@ int scratch_ptr(uint64_t** out) {
 int argmax_noalloc_launch(const float* x, int* result, int n, hipStream_t s) {
     if (!x || !result || n < 0 || !aligned(x, 4) || !aligned(result, 4)) return FENCE_ERROR_INVALID_VALUE;
     uint64_t* parts = nullptr;
-    const int st = scratch_ptr(&parts);
+    const int st = scratch_ptr(s, &parts);
     if (st != FENCE_SUCCESS) return st;
     // every n fits: the grid is capped at kArgmaxMaxParts workgroups
     return argmax_parts_launch(x, result, n, parts, argmax_parts(n, kArgmaxMaxParts), s);

@@ -1,0 +1,74 @@
+// calib.hip -- plain float4 streams for measuring the attainable HBM rate on
+// gfx950.  No reference counterpart: a benchmark times these next to the
+// ops, so each op's bandwidth can be read against what a stream of the same
+// read/write mix reaches on the same device, rather than only against the
+// 8 TB/s datasheet peak.
+//
+//   b != null: out[i] = a[i] + b[i]   (2 reads, 1 write: SwiGLU's traffic)
+//   b == null: out[i] = a[i]          (1 read, 1 write; out == a is the
+//                                      in-place form, RoPE's traffic)
+//
+// Each lane moves VPT float4s of every stream with non-temporal 128-bit loads
+// and stores (the elementwise kernels' memory access), THREADS lanes per
+// workgroup, one workgroup per THREADS * VPT float4s.  The launch shape is an
+// argument so the caller can sweep it and keep the fastest.
+#include "common.hpp"
+
+namespace fence {
+namespace {
+
+template <int THREADS, int VPT, bool TWO>
+__global__ __launch_bounds__(THREADS) void calib_stream_kernel(float* out, const float* a, const float* b,
+                                                               int64_t n4) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (THREADS * VPT) + threadIdx.x;
+    f4 v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t i = base + static_cast<int64_t>(j) * THREADS;
+        if (i < n4) {
+            v[j] = ld4<true>(a + 4 * i);
+            if constexpr (TWO) v[j] += ld4<true>(b + 4 * i);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t i = base + static_cast<int64_t>(j) * THREADS;
+        if (i < n4) st4<true>(out + 4 * i, v[j]);
+    }
+}
+
+template <int THREADS, int VPT>
+int calib_launch(float* out, const float* a, const float* b, int64_t n4, hipStream_t s) {
+    const unsigned grid = grid_1d(n4, THREADS * VPT);
+    if (b) return launch(calib_stream_kernel<THREADS, VPT, true>, dim3(grid), dim3(THREADS), 0, s, out, a, b, n4);
+    return launch(calib_stream_kernel<THREADS, VPT, false>, dim3(grid), dim3(THREADS), 0, s, out, a, b, n4);
+}
+
+template <int THREADS>
+int calib_vpt(int vpt, float* out, const float* a, const float* b, int64_t n4, hipStream_t s) {
+    switch (vpt) {
+        case 1: return calib_launch<THREADS, 1>(out, a, b, n4, s);
+        case 2: return calib_launch<THREADS, 2>(out, a, b, n4, s);
+        case 4: return calib_launch<THREADS, 4>(out, a, b, n4, s);
+        default: return FENCE_ERROR_INVALID_VALUE;
+    }
+}
+
+}  // namespace
+}  // namespace fence
+
+extern "C" int fence_calib_stream(float* out, const float* a, const float* b, int64_t n, int threads, int vpt,
+                                  hipStream_t stream) {
+    using namespace fence;
+    if (!out || !a || n < 0 || n % 4 != 0) return FENCE_ERROR_INVALID_VALUE;
+    if (!aligned(out, 16) || !aligned(a, 16) || (b && !aligned(b, 16))) return FENCE_ERROR_INVALID_VALUE;
+    const int64_t n4 = n / 4;
+    // one launch's grid must stay within a dispatch's 32-bit lane count
+    if (n4 > kMaxLaunchLanes) return FENCE_ERROR_INVALID_VALUE;
+    if (n4 == 0) return FENCE_SUCCESS;
+    switch (threads) {
+        case 64: return calib_vpt<64>(vpt, out, a, b, n4, stream);
+        case 256: return calib_vpt<256>(vpt, out, a, b, n4, stream);
+        default: return FENCE_ERROR_INVALID_VALUE;
+    }
+}

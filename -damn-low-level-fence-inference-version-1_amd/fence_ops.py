@@ -70,6 +70,7 @@ SIGNATURES = {
     "fence_rope_inv_freq": (_P, _I, _F),
     "fence_time_next_launch": (_P, _P),
     "fence_time_next_launches": (_P, _P, _I),
+    "fence_calib_stream": (_P, _P, _P, _L, _I, _I, _P),
     "fence_status_string": (_I,),
     "fence_version": (),
 }
@@ -312,6 +313,12 @@ def time_next_launches(start, stop, count) -> None:
     """Hook the next `count` launches: start at the first kernel's start,
     stop at the last one's end."""
     _call("fence_time_next_launches", start, stop, count)
+
+
+def calib_stream(out, a, b, n, threads=64, vpt=1, stream=None) -> None:
+    """Plain stream out = a + b (b given) or out = a (b None) for bandwidth
+    calibration; see include/fence/ops.h."""
+    _call("fence_calib_stream", out, a, b, n, threads, vpt, stream)
 
 
 def rope_inv_freq(head_dim: int, freq_base: float):

@@ -382,6 +382,27 @@ def main():
     per_op["softmax"]["generic_bytes"] = SOFTMAX_GENERIC_BYTES
     hev.destroy_all()
     dom = per_op[DOMINANT]
+
+    # The same K steps warm: one buffer set every step (after the cold run,
+    # so the headline above is untouched).
+    warm = None
+    if not args.warm:
+        b = sets[0]
+        for op in ops:
+            launch(op, b)
+        torch.cuda.synchronize()
+        w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0.record(stream)
+        for _ in range(args.steps):
+            for op in ops:
+                launch(op, b)
+        w1.record(stream)
+        torch.cuda.synchronize()
+        wms = w0.elapsed_time(w1) / args.steps
+        wv = STEP_BYTES / (wms * 1e-3) / 1e9
+        warm = {"ms_per_step": round(wms, 5), "value": round(wv, 1), "frac_peak": round(wv / PEAK_HBM_GBPS, 4),
+                "steps": args.steps, "cache": "warm (one buffer set, every step)",
+                "note": "one set is 2.55 GB, ten times the 256 MB Infinity Cache: little survives a step"}
     del sets, probe
     torch.cuda.empty_cache()
 
@@ -414,7 +435,15 @@ def main():
     decode = section("decode_op_set", lambda: decode_op_set(torch, F, gen, args.decode_reps))
     lm_head = section("lm_head_gemv", lambda: lm_head_gemv(torch, F, gen, args.lm_head_reps))
     decode_model = section("decode_qwen3_4b", lambda: decode_qwen3_4b(torch, args.decode_tokens))
-    copy_gbps = section("copy_calibration", lambda: copy_calibration(torch))
+    ceiling = section("practical_ceiling", lambda: practical_ceiling(torch, F, max(20, min(args.steps, 50))))
+    if "stream_2r1w" in ceiling:
+        c2, c1 = ceiling["stream_2r1w"]["GBps"], ceiling["stream_1r1w_inplace"]["GBps"]
+        roofline["ceiling_GBps"] = c2
+        roofline["frac_of_ceiling"] = round(dom["GBps"] / c2, 4)
+        roofline["ceiling_source"] = "practical_ceiling.stream_2r1w (a plain 2-read/1-write float4 stream, " \
+                                     "same size, same cold rotation)"
+        per_op["swiglu"]["frac_of_ceiling"] = round(per_op["swiglu"]["GBps"] / c2, 4)
+        per_op["rope"]["frac_of_ceiling"] = round(per_op["rope"]["GBps"] / c1, 4)
 
     cpu = None if args.no_cpu else section("cpu_baseline", lambda: cpu_baseline(args.cpu_seconds))
     cpu_all = None if args.no_cpu else section("cpu_baseline_all_cores",
@@ -452,7 +481,8 @@ def main():
         "decode_op_set_llama3_8b": decode,
         "lm_head_gemv_q8_0": lm_head,
         "decode_qwen3_4b": decode_model,
-        "copy_calibration_GBps": copy_gbps,
+        "practical_ceiling": ceiling,
+        "warm": warm,
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,
         "wall_s_timed": round(wall, 4),
@@ -597,6 +627,15 @@ def measure_configs(torch, F, reps, extended, back_to_back_timing=True):
             lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), 4, sh),
             "swiglu_vec_kernel", warm=True, b2b=True)
 
+    # The cold per-launch floors: one float4 of swiglu after the untimed 1 GiB
+    # scrub, so its load comes from HBM with cold caches and TLBs -- the
+    # load -> store chain of every streaming op.  The one-id gather and the
+    # one-token RMSNorm -> RoPE (their own chains) follow with configs[1].
+    measure("floor", "swiglu_one_float4_cold", "swiglu n=4 cold (load -> store)", 48,
+            lambda: dict(g=randn(4), u=randn(4), o=torch.empty(4, **dev)),
+            lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), 4, sh),
+            "swiglu_vec_kernel")
+
     # ---- Qwen3-4B decode, one token, fp32
     E0, F0, V0 = 2560, 9728, 151936
     pos0 = int(torch.randint(0, 4096, (1,), generator=torch.Generator().manual_seed(0)).item())
@@ -686,12 +725,26 @@ def measure_configs(torch, F, reps, extended, back_to_back_timing=True):
                          o=torch.empty(T1, H1, **dev)),
             lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), T1, H1, sh),
             "q8_gather_kernel", b2b=True)
+    # the gather's own chain for one token, cold: id -> row -> store
+    measure("floor", "gather_one_id_cold", "q8_0 gather 1 id x 4096 cold (id -> row -> store)",
+            H1 * 4 + H1 // 32 * 34 + 4,
+            lambda: dict(ids=torch.randint(0, V1, (1,), dtype=torch.int32, **dev, generator=gen),
+                         o=torch.empty(1, H1, **dev)),
+            lambda b: F.embed_q8_0_gather(b["o"].data_ptr(), tab1.data_ptr(), V1, b["ids"].data_ptr(), 1, H1, sh),
+            "q8_gather_kernel")
     del tab1
     measure(1, "norm_rope", "rms_norm->rope interleaved Q+K", 2 * T1 * H1 * 4 + H1 * 4 + 2 * T1 * NKV * HD * 4,
             lambda: dict(x=randn(T1, H1), o=torch.empty(T1, H1, **dev), k=randn(T1, NKV * HD)),
             lambda b: F.rms_norm_rope(b["o"].data_ptr(), b["x"].data_ptr(), w1.data_ptr(), b["k"].data_ptr(),
                                       T1, NQ, NKV, HD, 1e-5, None, 0, L3_THETA, F.ROPE_INTERLEAVED, sh),
             "head_ops_vec_kernel", b2b=True)
+    # its chain for one token, cold: load -> row reduction -> store
+    measure("floor", "norm_rope_one_token_cold", "rms_norm->rope 1 token cold (load -> reduce -> store)",
+            2 * H1 * 4 + H1 * 4 + 2 * NKV * HD * 4,
+            lambda: dict(x=randn(1, H1), o=torch.empty(1, H1, **dev), k=randn(1, NKV * HD)),
+            lambda b: F.rms_norm_rope(b["o"].data_ptr(), b["x"].data_ptr(), w1.data_ptr(), b["k"].data_ptr(),
+                                      1, NQ, NKV, HD, 1e-5, None, 0, L3_THETA, F.ROPE_INTERLEAVED, sh),
+            "head_ops_vec_kernel")
     measure(1, "swiglu", "swiglu 512x14336", 3 * T1 * F1 * 4,
             lambda: dict(g=randn(T1, F1), u=randn(T1, F1), o=torch.empty(T1, F1, **dev)),
             lambda b: F.swiglu(b["o"].data_ptr(), b["g"].data_ptr(), b["u"].data_ptr(), T1 * F1, sh),
@@ -767,7 +820,29 @@ def measure_configs(torch, F, reps, extended, back_to_back_timing=True):
     if scrub["buf"] is not None:
         scrub["buf"] = None
         torch.cuda.empty_cache()
+    attainable(results)
     return results
+
+
+# Each configs[1] op against its own cold chain: the floor launch whose
+# dependent chain it runs (measured cold in the same pass).
+FLOOR_OF = {"gather": "gather_one_id_cold", "norm_rope": "norm_rope_one_token_cold",
+            "swiglu": "swiglu_one_float4_cold"}
+
+
+def attainable(results):
+    """For each configs[1] op: attainable_us = cold floor of its chain + its
+    bytes at the 8 TB/s peak, and the op's fraction of that (attainable /
+    measured; 1.0 = at the bound).  Adds the fields to the op's record."""
+    floors = {r["key"]: r for r in results if r["config"] == "floor"}
+    for r in results:
+        fk = FLOOR_OF.get(r["key"]) if r["config"] == 1 else None
+        if fk not in floors:
+            continue
+        fl = floors[fk]["us_mean"]
+        att = fl + r["bytes"] / (PEAK_HBM_GBPS * 1e9) * 1e6
+        r["attainable"] = {"floor": fk, "floor_us": fl, "bytes_at_peak_us": round(att - fl, 3),
+                           "attainable_us": round(att, 3), "frac_of_attainable": round(att / r["us_mean"], 4)}
 
 
 def decode_qwen3_4b(torch, tokens):
@@ -986,6 +1061,92 @@ def q6k_bytes(m, k):
 def gemv_bytes(m, k):
     """Algorithmic bytes of y[m] = W x over a Q8_0 W: the table once, x, y."""
     return m * (k // 32) * 34 + 4 * k + 4 * m
+
+
+CALIB_SHAPES = ((64, 1), (64, 2), (64, 4), (256, 1), (256, 2), (256, 4))  # (lanes per workgroup, float4 per lane)
+
+
+def practical_ceiling(torch, F, reps):
+    """The attainable streaming rate on this device for the step's two traffic
+    mixes, each under a cold rotation (buffer sets of more than 1 GiB in
+    total, as the headline):
+      2 reads + 1 write at SwiGLU's size, [8192 x 14336] a + b -> out;
+      1 read + 1 write in place at RoPE's size, Q + K [8192 x 40 x 128].
+    For each: the library's plain float4 stream (fence_calib_stream) at six
+    launch shapes, the fastest kept, timed like the ops (kernel start/end
+    events of each launch); and torch's own elementwise kernel on the same
+    tensors (torch.mul(a, b, out=o); x.mul_(c)), timed by stream events around
+    each launch (which add ~1-2 us of dispatch to a ~200 us launch)."""
+    hev = HipEvents()
+    sh = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device="cuda").manual_seed(7)
+
+    def summary(ts, nbytes, **extra):
+        r = summarize(ts, nbytes, extra.pop("kernel"))
+        r.update(extra)
+        return r
+
+    def ours(sets, run, nbytes):
+        for b in sets:
+            run(b)
+        evs = [(hev.create(), hev.create()) for _ in range(reps)]
+        for i in range(reps):
+            F.time_next_launch(*evs[i])
+            run(sets[i % len(sets)])
+        torch.cuda.synchronize()
+        ts = [hev.elapsed_ms(a, b) * 1e3 for a, b in evs]
+        hev.destroy_all()
+        return ts
+
+    def theirs(sets, run):
+        for b in sets:
+            run(b)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for i in range(reps):
+            evs[i][0].record()
+            run(sets[i % len(sets)])
+            evs[i][1].record()
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) * 1e3 for a, b in evs]
+
+    out = {}
+    for mix, n, nstreams in (("2r1w", T4 * FFN4, 3), ("1r1w_inplace", T4 * (NQ + NKV) * HD, 2)):
+        nbytes = nstreams * n * 4
+        set_bytes = (3 if mix == "2r1w" else 1) * n * 4
+        nsets = max(2, -(-(1 << 30) // set_bytes) + 1)
+        if mix == "2r1w":
+            sets = [(torch.randn(n, device="cuda", generator=gen), torch.randn(n, device="cuda", generator=gen),
+                     torch.empty(n, device="cuda")) for _ in range(nsets)]
+            run_ours = lambda t, v, b: F.calib_stream(b[2].data_ptr(), b[0].data_ptr(), b[1].data_ptr(), n,  # noqa
+                                                       t, v, sh)
+            run_torch = lambda b: torch.mul(b[0], b[1], out=b[2])  # noqa: E731
+        else:
+            sets = [(torch.randn(n, device="cuda", generator=gen),) for _ in range(nsets)]
+            run_ours = lambda t, v, b: F.calib_stream(b[0].data_ptr(), b[0].data_ptr(), None, n, t, v, sh)  # noqa
+            run_torch = lambda b: b[0].mul_(1.0000001)  # noqa: E731
+        shapes = {}
+        best = None
+        for t, v in CALIB_SHAPES:
+            r = summary(ours(sets, lambda b, t=t, v=v: run_ours(t, v, b), nbytes), nbytes,
+                        kernel="calib_stream_kernel", threads=t, float4_per_lane=v)
+            shapes[f"{t}x{v}"] = r["GBps"]
+            if best is None or r["us_mean"] < best["us_mean"]:
+                best = r
+        best["GBps_by_shape"] = shapes
+        best["sets"] = nsets
+        best["timing"] = "kernel start/end events of each launch (hipExtLaunchKernel)"
+        out[f"stream_{mix}"] = best
+        tr = summary(theirs(sets, run_torch), nbytes, kernel="torch.mul" if mix == "2r1w" else "torch.mul_")
+        tr["sets"] = nsets
+        tr["timing"] = "stream events around each launch"
+        out[f"torch_{mix}"] = tr
+        print(f"[ceiling] {mix}: stream {best['GBps']:.1f} GB/s ({100 * best['frac_peak']:.1f}%, "
+              f"{best['threads']}x{best['float4_per_lane']}), torch {tr['GBps']:.1f} GB/s "
+              f"({100 * tr['frac_peak']:.1f}%)", file=sys.stderr, flush=True)
+        del sets
+        torch.cuda.empty_cache()
+    out["torch_copy_1GiB_GBps"] = copy_calibration(torch)
+    return out
 
 
 def copy_calibration(torch):

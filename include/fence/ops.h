@@ -169,7 +169,8 @@ int fence_argmax_ws(const float* x, int* result, int n, void* workspace, int64_t
  * a workspace.  Allocates nothing.  Each GPU holds one scratch for the life of
  * the process and every call on that GPU shares it: calls that overlap on one
  * GPU (two streams or threads at once) race; calls ordered on one stream do
- * not.  Same index as fence_argmax. */
+ * not.  The stream must belong to the current device (EINVAL otherwise): the
+ * scratch address used is the current device's.  Same index as fence_argmax. */
 int fence_argmax_noalloc(const float* x, int* result, int n, hipStream_t stream);
 
 /* Replaces residual_add, src/kernels/ops.cuh:265-270: x[i] += residual[i]. */
@@ -388,6 +389,17 @@ int fence_time_next_launch(hipEvent_t start, hipEvent_t stop);
  * that launches several kernels): start at the first kernel's start, stop at
  * the last one's end.  count < 1 is FENCE_ERROR_INVALID_VALUE. */
 int fence_time_next_launches(hipEvent_t start, hipEvent_t stop, int count);
+
+/* Calibration stream: out[i] = a[i] + b[i] (b != NULL: 2 reads, 1 write) or
+ * out[i] = a[i] (b == NULL: 1 read, 1 write; out == a is the in-place form)
+ * over n floats, with the elementwise kernels' memory access (non-temporal
+ * 128-bit loads and stores) at a chosen launch shape: `threads` lanes per
+ * workgroup (64 or 256), `vpt` float4s per lane (1, 2 or 4).  n % 4 == 0,
+ * every pointer 16-byte aligned and n / 4 <= 2^30, else EINVAL.  No
+ * counterpart in the reference; the benchmark times it to report the
+ * attainable streaming rate beside each op's. */
+int fence_calib_stream(float* out, const float* a, const float* b, int64_t n, int threads, int vpt,
+                       hipStream_t stream);
 
 /* Static text for a status code. */
 const char* fence_status_string(int status);

@@ -395,7 +395,11 @@ void fo_gqa_attention(float* out, const float* q, const uint16_t* k_cache,
     if (s != s_small) free(s);
 }
 
-/* src/kernels/ops.cuh:448-480: the largest value; ties go to the lowest index */
+/* argmax, src/kernels/ops.cuh:467-505: the reference's one 256-thread block.
+ * Ties follow its tree, not the lowest index: among the threads t = i mod 256
+ * holding the maximum, the one with the smallest 8-bit bit-reversal of t wins
+ * (maxima at 1 and 256 give 256, at 1 and 2 give 2); within a thread, the
+ * first index. */
 int fo_argmax(const float* x, int n) {
     /* src/kernels/ops.cuh:476-485, 256 threads (:502): thread t scans x[t],
      * x[t+256], .. keeping the first value strictly above its maximum. */

@@ -142,6 +142,11 @@ def _raw(name):
     ("fence_residual_rms_norm_f16", (16, 32, 48, 64, 80, 2, 0, 1e-6, None)),
     ("fence_swiglu_f16", (None, 16, 32, 48, 8, None)),
     ("fence_swiglu_f16", (0x1001, None, 32, 48, 8, None)),
+    ("fence_calib_stream", (16, 32, 48, 6, 64, 1, None)),          # n % 4 != 0
+    ("fence_calib_stream", (16, 0x1008, 48, 8, 64, 1, None)),      # a not 16-byte aligned
+    ("fence_calib_stream", (16, 32, 48, 8, 128, 1, None)),         # threads not 64 or 256
+    ("fence_calib_stream", (16, 32, None, 8, 64, 3, None)),        # vpt not 1, 2 or 4
+    ("fence_calib_stream", (16, 32, None, 8 << 30, 64, 1, None)),  # past one launch
 ])
 def test_invalid_arguments_rejected_on_host(fence, name, args):
     assert _raw(name)(*args) == EINVAL

@@ -53,3 +53,20 @@ def test_step_bytes_are_the_configs4_shapes():
     # interleaved RoPE in place on Q [8192 x 32 x 128] and K [8192 x 8 x 128]
     assert bench.BYTES["rope"] == 2 * 8192 * 40 * 128 * 4 == 335544320
     assert bench.STEP_BYTES == 805437440 + 1409286144 + 335544320
+
+
+def test_attainable_is_cold_floor_plus_bytes_at_peak():
+    """attainable_us = the op's own cold chain floor + its bytes at 8 TB/s;
+    frac_of_attainable = attainable / measured."""
+    res = [{"config": "floor", "key": "gather_one_id_cold", "us_mean": 4.0, "bytes": 16_000},
+           {"config": "floor", "key": "swiglu_one_float4_cold", "us_mean": 3.5, "bytes": 48},
+           {"config": 1, "key": "gather", "us_mean": 5.0, "bytes": 8_000_000},
+           {"config": 1, "key": "swiglu", "us_mean": 14.0, "bytes": 88_000_000},
+           {"config": 1, "key": "norm_rope", "us_mean": 6.0, "bytes": 21_000_000},  # its floor not measured
+           {"config": 2, "key": "swiglu", "us_mean": 90.0, "bytes": 600_000_000}]
+    bench.attainable(res)
+    g = res[2]["attainable"]
+    assert g["floor"] == "gather_one_id_cold" and g["attainable_us"] == 5.0 and g["frac_of_attainable"] == 1.0
+    s = res[3]["attainable"]
+    assert s["attainable_us"] == 3.5 + 11.0 and s["frac_of_attainable"] == round(14.5 / 14.0, 4)
+    assert "attainable" not in res[4] and "attainable" not in res[5]

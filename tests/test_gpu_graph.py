@@ -115,9 +115,10 @@ def test_decode_step_in_a_graph():
     normed = torch.empty(E, device="cuda")
     logits = torch.empty(V, device="cuda")
     tok = torch.empty(1, dtype=torch.int32, device="cuda")
+    tok_na = torch.empty(1, dtype=torch.int32, device="cuda")
     ws = torch.empty(4 * nq * ctx, device="cuda")
     LIVE.extend([Wq, Wk, Wv, Wo, Wg, Wu, Wd, table, an, fn, qn, kn, on, kc, vc, kc0, vc0, hidden, res, h1, h2, x16,
-                 q, k, v, att16, o, d, act16, normed, logits, tok, ws])
+                 q, k, v, att16, o, d, act16, normed, logits, tok, tok_na, ws])
     rin_a = F.rms_input(hidden.data_ptr(), res.data_ptr(), h1.data_ptr(), an.data_ptr(), x16.data_ptr(), 1e-6)
     rin_f = F.rms_input(h1.data_ptr(), o.data_ptr(), h2.data_ptr(), fn.data_ptr(), x16.data_ptr(), 1e-6)
 
@@ -138,7 +139,11 @@ def test_decode_step_in_a_graph():
                                 1e-6, sh)
         F.gemv_q8_0(table.data_ptr(), normed.data_ptr(), logits.data_ptr(), V, E, sh)
         F.argmax_ws(logits.data_ptr(), tok.data_ptr(), V, ws.data_ptr(), ws.numel() * 4, sh)
+        # the allocation-free form: its first call on the device (possibly this
+        # capture) looks up the scratch address; its kernels are captured too
+        F.argmax_noalloc(logits.data_ptr(), tok_na.data_ptr(), V, sh)
 
     # every run recomputes h1, h2 (h2 = h1 + o, then += d) and q/k/v from the unchanged inputs;
     # only the caches' row pos carries over, and reset() restores it
-    check_graph(run, [q, k, v, att16, o, act16, d, normed, logits, tok, kc, vc, h1, h2], reset)
+    check_graph(run, [q, k, v, att16, o, act16, d, normed, logits, tok, tok_na, kc, vc, h1, h2], reset)
+    assert int(tok_na.item()) == int(tok.item())

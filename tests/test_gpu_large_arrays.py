@@ -74,3 +74,36 @@ def test_rope_past_one_launch():
         assert np.array_equal(k[a:b].cpu().numpy().view(np.uint32), k0.cpu().numpy().view(np.uint32)), f"k {a}..{b}"
     del q, k
     torch.cuda.empty_cache()
+
+
+def test_argmax_near_int_max():
+    """argmax over n = 2^31 - 1 floats (8 GiB): a lane's tail index 4 * (n / 4)
+    + lane and a grid-strided index + stride pass INT_MAX here, so they must be
+    computed in 64 bits.  Maxima at 1 and n - 1 tie; the reference's 256-thread
+    rule gives n - 1 (thread 254 = 0b11111110 reverses to 127, below thread
+    1's 128).  Every entry point, aligned (float4 path) and one float off
+    (scalar path)."""
+    torch = torch_mod()
+    if _free_gib(torch) < 10:
+        pytest.skip("needs 9 GiB of free device memory")
+    n = (1 << 31) - 1
+    x = torch.full((n + 1,), -1.0, device="cuda")
+    r = torch.empty(1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(1024, dtype=torch.int64, device="cuda")
+    for off in (0, 1):
+        x.fill_(-1.0)
+        x[off + 1] = 9.0
+        x[off + n - 1] = 9.0
+        ptr = x.data_ptr() + 4 * off
+        for entry in ("one_workgroup", "workspace", "noalloc"):
+            r.fill_(-7)
+            if entry == "one_workgroup":
+                F.argmax(ptr, r.data_ptr(), n, stream())
+            elif entry == "workspace":
+                F.argmax_ws(ptr, r.data_ptr(), n, ws.data_ptr(), 8 * 1024, stream())
+            else:
+                F.argmax_noalloc(ptr, r.data_ptr(), n, stream())
+            torch.cuda.synchronize()
+            assert int(r.item()) == n - 1, f"{entry}, offset {off}"
+    del x, r, ws
+    torch.cuda.empty_cache()
