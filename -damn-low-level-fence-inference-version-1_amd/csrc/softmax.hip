@@ -10,7 +10,9 @@
 // written once.  A row gets TPR lanes holding ~2 float4 each (generic) or ~4
 // (causal, whose rows are short on average); rows of up to 256 lanes are
 // packed several to a 256-thread workgroup.  All loads of a lane are issued
-// before any of them is consumed.
+// before any of them is consumed.  e^x comes from exp_hw (common.hpp): the
+// hardware base-2 exponential, within ~1e-6 relative of expf for the scores'
+// range (x - m <= 0; masked -inf keys give exactly 0).
 // Causal form: query i of sq sees keys 0 .. i + (sk - sq).  Keys past that
 // bound are not read and are written as exactly 0.
 #include "common.hpp"
@@ -85,10 +87,10 @@ __global__ __launch_bounds__(TPR == 0 ? 1024 : 256) void softmax_vec_kernel(
         for (int j = 0; j < MAXV; ++j) {
             // whole chunk j of this row beyond the causal bound: nothing to do
             if (j < vpt && 4 * j * tpr < valid) {
-                v[j].x = expf(v[j].x - m);
-                v[j].y = expf(v[j].y - m);
-                v[j].z = expf(v[j].z - m);
-                v[j].w = expf(v[j].w - m);
+                v[j].x = exp_hw(v[j].x - m);
+                v[j].y = exp_hw(v[j].y - m);
+                v[j].z = exp_hw(v[j].z - m);
+                v[j].w = exp_hw(v[j].w - m);
                 s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
             }
         }
@@ -133,10 +135,10 @@ __global__ __launch_bounds__(256) void softmax_scalar_kernel(float* x, int64_t r
         m = block_reduce<4>(m, OpMax(), red);
         __syncthreads();
         float s = 0.0f;
-        for (int i = threadIdx.x; i < valid; i += 256) s += expf(row[i] - m);
+        for (int i = threadIdx.x; i < valid; i += 256) s += exp_hw(row[i] - m);
         s = block_reduce<4>(s, OpAdd(), red);
         const float inv = 1.0f / s;
-        for (int i = threadIdx.x; i < n; i += 256) row[i] = (i < valid) ? expf(row[i] - m) * inv : 0.0f;
+        for (int i = threadIdx.x; i < n; i += 256) row[i] = (i < valid) ? exp_hw(row[i] - m) * inv : 0.0f;
         __syncthreads();
     }
 }
