@@ -47,6 +47,17 @@
 #ifndef FENCE_GEMV_Q6K_RESIDENT
 #define FENCE_GEMV_Q6K_RESIDENT 1
 #endif
+// 1: the resident grid is trimmed so every workgroup gets the same number of
+// row groups: with G groups and room for W workgroups, ceil(G / W) rounds
+// need only ceil(G / rounds) workgroups.  0 (kept): W workgroups, the last
+// round partly empty.  Results do not depend on the grid.  Measured on
+// MI355X, Qwen3-4B decode steps (bench.py --decode-only, 64 tokens, two
+// interleaved runs each): 1,852 and 1,854 us per token with 1 against 1,768
+// and 1,767 with 0 -- wave lifetimes vary by several us within a launch
+// whatever the group count, so fewer workgroups only lose parallelism.
+#ifndef FENCE_GEMV_Q6K_BALANCED
+#define FENCE_GEMV_Q6K_BALANCED 0
+#endif
 // Launches of at most this many rows of 13-16 blocks take the one-wave layout
 // spread over four waves per row (XW below; same results, bit for bit).
 // Measured on MI355X, p50: the 2560 x 4096 o projection runs in 4.96 us with
@@ -56,10 +67,60 @@
 #define FENCE_GEMV_Q6K_XW_ROWS 8192
 #endif
 
+// 1: every wave of the staged kernel records its entry and exit times on the
+// device's constant wall clock (100 MHz), its hardware placement and its
+// row-group count into `wave_clock` (read back by fence_wave_clock_read).
+// Only the instrumented library (libfence_ops_waveclock.so) is built with it;
+// the product library is not, and its kernels are unchanged.
+#ifndef FENCE_WAVE_CLOCK
+#define FENCE_WAVE_CLOCK 0
+#endif
+
 namespace fence {
 namespace {
 
 constexpr int kThreads = 256;
+
+#if FENCE_WAVE_CLOCK
+// One record of four words per wave of a launch (the last launch's):
+// entry time, exit time, HW_ID | XCC_ID << 32, row groups computed.
+constexpr int kWaveClockMax = 1 << 16;
+static __device__ __align__(256) uint64_t wave_clock[4 * kWaveClockMax];
+#endif
+
+// Wave entry and exit for FENCE_WAVE_CLOCK builds (empty otherwise).  Each
+// writes its words straight away (lane 0, vector stores) and keeps nothing
+// live across the kernel, to leave the kernel's register allocation as it is.
+[[maybe_unused]] __device__ __forceinline__ void wave_clock_enter(int64_t wave, int lane) {
+#if FENCE_WAVE_CLOCK
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && wave < kWaveClockMax) wave_clock[4 * wave] = t;
+#else
+    (void)wave;
+    (void)lane;
+#endif
+}
+
+// groups: the wave's row groups g = blockIdx.x + k * gridDim.x < n_groups
+[[maybe_unused]] __device__ __forceinline__ void wave_clock_leave(int64_t wave, int lane, int64_t n_groups) {
+#if FENCE_WAVE_CLOCK
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    // HW_ID (hardware register 4) and XCC_ID (20), all 32 bits of each
+    const uint32_t hw = __builtin_amdgcn_s_getreg(4 | (31 << 11));
+    const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (31 << 11));
+    const int64_t groups = n_groups > blockIdx.x ? (n_groups - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    if (lane == 0 && wave < kWaveClockMax) {
+        uint64_t* r = wave_clock + 4 * wave;
+        r[1] = t;
+        r[2] = static_cast<uint64_t>(hw) | (static_cast<uint64_t>(xcc) << 32);
+        r[3] = static_cast<uint64_t>(groups);
+    }
+#else
+    (void)wave;
+    (void)lane;
+    (void)n_groups;
+#endif
+}
 constexpr int kBlockBytes = 210;
 constexpr int kMaxSegBlocks = 16;  // blocks of one row staged by one wave
 
@@ -91,11 +152,14 @@ __device__ __forceinline__ h2 q6_pair(uint32_t w, uint32_t sel) {
 // sum over (1024 + q) * x then starts from it, which leaves
 // sum (q - 32) * x: the -32 of the format and the 1024 of the binary16
 // encoding cancel exactly when x is a unit vector, and otherwise to within
-// fp32 rounding of terms of size 1056 |x|.
+// fp32 rounding of terms of size 1056 |x|.  Two v_dot2_f32_f16 against
+// (-1056, -1056), which binary16 holds exactly (every product is exact in
+// fp32): 2 operations per column where converting and adding the four x
+// takes 8.
 __device__ __forceinline__ float q6_col_bias(uint32_t x01, uint32_t x23) {
-    const h2 a = __builtin_bit_cast(h2, x01), b = __builtin_bit_cast(h2, x23);
-    return -1056.0f * ((static_cast<float>(a.x) + static_cast<float>(a.y)) +
-                       (static_cast<float>(b.x) + static_cast<float>(b.y)));
+    const h2 k = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
+    const float t = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x01), k, 0.0f, false);
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x23), k, t, false);
 }
 
 // d * sum_c sc_c * sum_k (q - 32) * x over the lane's 16 weights of one block,
@@ -243,7 +307,9 @@ constexpr int staged_waves() { return NORM && !PAIR && WPR == 1 ? 8 : (PAIR && W
 // 400, in-process A/B: the o projection 2560 x 4096 4.92 -> 4.60 us, Llama-3-8B
 // 4096 x 4096 6.44 -> 5.80 us; the same prefetch in the other layouts cost
 // more registers than it saved (gate/up pair, 9728 x 2560) or changed nothing.
-template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
+// CLOCK: the instrumented copy (FENCE_WAVE_CLOCK builds launch it on the grid
+// the plain kernel gets); every product launch has CLOCK = false.
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false, bool CLOCK = false>
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
     static_assert(!XW || (PASSES * WPR == 4 && !PAIR && NORM == 0), "XW: four passes, plain rows");
@@ -266,6 +332,7 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
     __shared__ float xr[XW ? NW : 1][XW ? PASSES : 1][kWave];  // XW: each pass's lane values
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));  // wave-uniform
+    if constexpr (CLOCK) wave_clock_enter(static_cast<int64_t>(blockIdx.x) * NW + wid, lane);
     const int seg = wid % WPR;
     const int rslot = wid / WPR;
     uint8_t* buf = lds + wid * kBufBytes;
@@ -548,6 +615,8 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
         }
         for (; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::false_type{});
     }
+    if constexpr (CLOCK)
+        wave_clock_leave(static_cast<int64_t>(blockIdx.x) * NW + wid, lane, (n_out + kOutPerGroup - 1) / kOutPerGroup);
 }
 
 // The lane's value of block b of row lr (its 16 weights), for the direct
@@ -632,11 +701,12 @@ __global__ __launch_bounds__(kThreads) void gemv_q6k_direct_kernel(const Q6Job j
     }
 }
 
-// A resident grid for `kernel` of `threads` per workgroup: CUs x the
-// occupancy per CU (cached per device in `cache`), at most `groups`.
-template <class Kernel, class... Args>
-int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t groups, hipStream_t s,
-                const Args&... args) {
+// A resident grid of `threads`-lane workgroups for `occ_kernel`: CUs x its
+// occupancy per CU (cached per device in `cache`), at most `groups`; launches
+// `kernel` on it (the same kernel, or its instrumented copy).
+template <class OccKernel, class Kernel, class... Args>
+int launch_grid_as(OccKernel occ_kernel, Kernel kernel, int threads, std::atomic<int>* cache, int64_t groups,
+                   hipStream_t s, const Args&... args) {
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e);
     if (dev < 0 || dev >= 64) return FENCE_ERROR_INVALID_VALUE;
@@ -645,15 +715,26 @@ int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t gro
         int cus = 0, per_cu = 0;
         if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev); e != hipSuccess)
             return hip_status(e);
-        if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0);
+        if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, occ_kernel, threads, 0);
             e != hipSuccess)
             return hip_status(e);
         g = cus * (per_cu > 0 ? per_cu : 1);
         cache[dev].store(g, std::memory_order_relaxed);
     }
     if (!FENCE_GEMV_Q6K_RESIDENT) g = 0x7fffffff;
-    const unsigned grid = static_cast<unsigned>(groups < g ? groups : g);
+    int64_t w = groups < g ? groups : g;
+    if (FENCE_GEMV_Q6K_BALANCED && w > 0) {
+        const int64_t rounds = (groups + w - 1) / w;
+        w = (groups + rounds - 1) / rounds;
+    }
+    const unsigned grid = static_cast<unsigned>(w);
     return launch(kernel, dim3(grid), dim3(threads), 0, s, args...);
+}
+
+template <class Kernel, class... Args>
+int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t groups, hipStream_t s,
+                const Args&... args) {
+    return launch_grid_as(kernel, kernel, threads, cache, groups, s, args...);
 }
 
 template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
@@ -661,8 +742,9 @@ int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, co
     static std::atomic<int> cache[64];
     constexpr int nw = staged_waves<WPR, PAIR, NORM>();
     constexpr int out_per_group = PAIR ? nw / WPR / 2 : nw / WPR;
-    return launch_grid(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW>, kWave * nw, cache,
-                       (n_out + out_per_group - 1) / out_per_group, s, job, x, nb, rin);
+    return launch_grid_as(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW, false>,
+                          gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW, FENCE_WAVE_CLOCK != 0>,
+                          kWave * nw, cache, (n_out + out_per_group - 1) / out_per_group, s, job, x, nb, rin);
 }
 
 // The staged kernel for a row of nb blocks, at q6_wpr / q6_passes.  Only the
@@ -888,3 +970,22 @@ extern "C" int fence_gemv_q6k_swiglu_rms_f16(const void* W_gate, const void* W_u
     if (int st = rms_input(in, K, &r)) return st;
     return gemv_q6k_run(job, nullptr, K, true, stream, &r);
 }
+
+#if FENCE_WAVE_CLOCK
+// Instrumented library only (include/fence/wave_clock.h).
+extern "C" int fence_wave_clock_clear(void) {
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(fence::wave_clock)); e != hipSuccess)
+        return fence::hip_status(e);
+    if (hipError_t e = hipMemset(p, 0, sizeof(fence::wave_clock)); e != hipSuccess) return fence::hip_status(e);
+    return fence::hip_status(hipDeviceSynchronize());
+}
+
+extern "C" int fence_wave_clock_read(uint64_t* dst, int64_t max_waves) {
+    if (!dst || max_waves < 0) return FENCE_ERROR_INVALID_VALUE;
+    const int64_t n = max_waves < fence::kWaveClockMax ? max_waves : fence::kWaveClockMax;
+    if (hipError_t e = hipDeviceSynchronize(); e != hipSuccess) return fence::hip_status(e);
+    return fence::hip_status(hipMemcpyFromSymbol(dst, HIP_SYMBOL(fence::wave_clock), 32 * n, 0,
+                                                 hipMemcpyDeviceToHost));
+}
+#endif

@@ -13,7 +13,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libfence_ops.so")
+# FENCE_OPS_LIB: another build of the same library (a Makefile TAG variant,
+# for A/B timing); unset, the package's own.
+LIB_PATH = os.environ.get("FENCE_OPS_LIB") or os.path.join(HERE, "libfence_ops.so")
 
 SUCCESS = 0
 EINVAL = 22

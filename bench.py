@@ -94,6 +94,13 @@ def parse():
                     help="also measure the decode-path ops (GEMVs, attention, epilogues) of every "
                          "config and write the per-op report (JSON) to PATH; a table goes to stderr")
     ap.add_argument("--all-reps", type=int, default=50)
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the Qwen3-4B-shaped decode steps (decode_qwen3_4b) as one JSON line")
+    ap.add_argument("--wave-clock", metavar="PATH", default=None,
+                    help="only the per-wave clock of the Qwen3-4B decode layer's four Q6_K GEMV launches, "
+                         "through the instrumented library (libfence_ops_waveclock.so); summary JSON to PATH")
+    ap.add_argument("--wave-clock-raw", metavar="PATH", default=None,
+                    help="with --wave-clock: also save each launch's last raw records (npz) to PATH")
     ap.add_argument("--all-only", metavar="PATH", default=None,
                     help="only the device-copy calibration and the --all measurements (written to PATH), "
                          "no JSON line: the run the per-op rocprofv3 summaries profile")
@@ -314,7 +321,17 @@ def main():
     import fence_ops as F
 
     torch.cuda.set_device(0)
+    if args.wave_clock:
+        res = wave_clock(torch, F, max(args.all_reps, 5), args.wave_clock_raw)
+        with open(args.wave_clock, "w") as fh:
+            json.dump(res, fh, indent=1)
+        print(f"wrote {args.wave_clock}", file=sys.stderr)
+        return
     F.lib()
+    if args.decode_only:
+        print(json.dumps({"library": F.LIB_PATH, "decode_qwen3_4b": decode_qwen3_4b(torch, args.decode_tokens)}),
+              flush=True)
+        return
     if args.all_only:
         copy_gbps = copy_calibration(torch)
         # no back-to-back passes here: the profiler runs match dispatches to ops by count
@@ -1041,6 +1058,124 @@ def decode_op_set(torch, F, gen, reps):
         out["graph_sustained_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
     except Exception as exc:  # graph capture is optional for the report
         out["graph_error"] = str(exc)[:200]
+    return out
+
+
+WAVE_CLOCK_LIB = os.path.join(PKG, "libfence_ops_waveclock.so")
+
+
+def wave_clock(torch, F, reps, raw_path=None):
+    """Where a decode layer's Q6_K GEMV launches spend their time, wave by
+    wave.  Loads the instrumented library (gemv_q6k.hip built with
+    FENCE_WAVE_CLOCK=1: every wave of the staged kernel records its entry and
+    exit on the device's constant wall clock, its XCC / shader engine / CU and
+    its row-group count; include/fence/wave_clock.h) and runs the four GEMV
+    launches of a Qwen3-4B decode layer as the fused sequence issues them --
+    q/k/v with the RMSNorm prologue, o, gate/up + SwiGLU with the RMSNorm
+    prologue, down -- with cold weights (sets rotated over more than 1 GiB)
+    and warm inputs, each launch also timed by its kernel start/end events.
+    Per launch (medians over `reps`): the span from the first wave's entry to
+    the last wave's exit against the event time; the dispatch ramp (entry
+    offsets); each wave's lifetime and its time per row group; the tail
+    (exit offsets from the last exit); mean resident waves per CU over the
+    span against the waves launched per CU."""
+    import ctypes
+
+    import numpy as np
+    L = F.lib(WAVE_CLOCK_LIB)  # the first load of the process: every call below goes to it
+    L.fence_wave_clock_read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    L.fence_wave_clock_clear.argtypes = []
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    khz = ctypes.c_int()
+    if hip.hipDeviceGetAttribute(ctypes.byref(khz), 10017, 0) != 0 or khz.value <= 0:  # hipDeviceAttributeWallClockRate
+        raise RuntimeError("no wall clock rate")
+    us_per_tick = 1e3 / khz.value
+    hev = HipEvents()
+    sh = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    E, QD, KVD, FF = 2560, 4096, 1024, 9728
+    hid, res, w1, w2 = (torch.randn(E, device="cuda", generator=gen) for _ in range(4))
+    hout = torch.empty(E, device="cuda")
+    x16 = torch.empty(E, dtype=torch.int16, device="cuda")
+    att16 = torch.randn(QD, device="cuda", generator=gen).half()
+    act16 = torch.randn(FF, device="cuda", generator=gen).half()
+    q, k, v = (torch.empty(n, device="cuda") for n in (QD, KVD, KVD))
+    o, d = torch.empty(E, device="cuda"), torch.empty(E, device="cuda")
+    gu16 = torch.empty(FF, dtype=torch.int16, device="cuda")
+    rin1 = F.rms_input(hid.data_ptr(), res.data_ptr(), hout.data_ptr(), w1.data_ptr(), x16.data_ptr(), 1e-6)
+    rin2 = F.rms_input(hid.data_ptr(), res.data_ptr(), hout.data_ptr(), w2.data_ptr(), x16.data_ptr(), 1e-6)
+
+    def weights(shapes):
+        return [make_q6k_table(torch, gen, m, kk) for m, kk in shapes]
+
+    ops = [
+        ("q/k/v + RMSNorm prologue", [(QD, E), (KVD, E), (KVD, E)],
+         lambda W: F.gemv_q6k_multi_rms([t.data_ptr() for t in W], [q.data_ptr(), k.data_ptr(), v.data_ptr()],
+                                        [QD, KVD, KVD], rin1, E, stream=sh)),
+        ("o", [(E, QD)], lambda W: F.gemv_q6k(W[0].data_ptr(), att16.data_ptr(), o.data_ptr(), E, QD, sh)),
+        ("gate/up + RMSNorm prologue + SwiGLU", [(FF, E), (FF, E)],
+         lambda W: F.gemv_q6k_swiglu_rms_f16(W[0].data_ptr(), W[1].data_ptr(), rin2, gu16.data_ptr(), None, FF, E,
+                                             sh)),
+        ("down", [(E, FF)], lambda W: F.gemv_q6k(W[0].data_ptr(), act16.data_ptr(), d.data_ptr(), E, FF, sh)),
+    ]
+    buf = (ctypes.c_uint64 * (4 * 65536))()
+    out = {"clock_kHz": khz.value, "reps": reps, "timing": "kernel start/end events (hipExtLaunchKernel) and "
+           "per-wave s_memrealtime entry/exit", "ops": {}}
+    raw = {}  # the last launch's records per op, for a closer look (--wave-clock-raw)
+
+    for name, shapes, run in ops:
+        nbytes = sum(q6k_bytes(m, kk) for m, kk in shapes)
+        nsets = max(2, -(-(1 << 30) // nbytes) + 1)
+        sets = [weights(shapes) for _ in range(nsets)]
+        for Wset in sets:
+            run(Wset)
+        per = []
+        for i in range(reps):
+            if L.fence_wave_clock_clear() != 0:
+                raise RuntimeError("fence_wave_clock_clear failed")
+            e0, e1 = hev.create(), hev.create()
+            F.time_next_launch(e0, e1)
+            run(sets[i % nsets])
+            torch.cuda.synchronize()
+            ev_us = hev.elapsed_ms(e0, e1) * 1e3
+            if L.fence_wave_clock_read(ctypes.cast(buf, ctypes.c_void_p), 65536) != 0:
+                raise RuntimeError("fence_wave_clock_read failed")
+            r = np.ctypeslib.as_array(buf).reshape(-1, 4)
+            r = r[r[:, 0] != 0].astype(np.int64)
+            t0, t1 = int(r[:, 0].min()), int(r[:, 1].max())
+            span = (t1 - t0) * us_per_tick
+            life = (r[:, 1] - r[:, 0]) * us_per_tick
+            ramp = (r[:, 0] - t0) * us_per_tick
+            tail = (t1 - r[:, 1]) * us_per_tick
+            groups = r[:, 3]
+            hw, xcc = r[:, 2] & 0xFFFFFFFF, (r[:, 2] >> 32) & 0xF
+            cu = ((xcc * 8 + ((hw >> 13) & 7)) * 2 + ((hw >> 12) & 1)) * 16 + ((hw >> 8) & 15)
+            _, per_cu = np.unique(cu, return_counts=True)
+            per.append({"event_us": ev_us, "span_us": span, "waves": len(r), "cus": len(per_cu),
+                        "waves_per_cu_max": int(per_cu.max()),
+                        "ramp_p50_us": float(np.percentile(ramp, 50)), "ramp_p90_us": float(np.percentile(ramp, 90)),
+                        "ramp_max_us": float(ramp.max()), "life_mean_us": float(life.mean()),
+                        "life_p10_us": float(np.percentile(life, 10)), "life_p90_us": float(np.percentile(life, 90)),
+                        "groups_min": int(groups.min()), "groups_max": int(groups.max()),
+                        "us_per_group_mean": float((life[groups > 0] / groups[groups > 0]).mean()),
+                        "tail_p50_us": float(np.percentile(tail, 50)), "tail_p90_us": float(np.percentile(tail, 90)),
+                        "resident_waves_per_cu_mean": float(life.sum() / span / len(per_cu)) if span > 0 else 0.0})
+            hev.destroy_all()
+        raw[name] = r.copy()
+        med = {key: round(float(np.median([p[key] for p in per])), 3) for key in per[0]}
+        med["bytes"] = nbytes
+        med["GBps_event"] = round(nbytes / (med["event_us"] * 1e-6) / 1e9, 1)
+        out["ops"][name] = med
+        print(f"[wave clock] {name:38s} event {med['event_us']:6.2f} us  span {med['span_us']:6.2f}  "
+              f"waves {int(med['waves'])} on {int(med['cus'])} CUs  ramp p50/p90/max {med['ramp_p50_us']:.2f}/"
+              f"{med['ramp_p90_us']:.2f}/{med['ramp_max_us']:.2f}  life {med['life_mean_us']:.2f} "
+              f"({int(med['groups_min'])}-{int(med['groups_max'])} groups, {med['us_per_group_mean']:.2f}/group)  "
+              f"tail p50/p90 {med['tail_p50_us']:.2f}/{med['tail_p90_us']:.2f}  resident/CU "
+              f"{med['resident_waves_per_cu_mean']:.1f}", file=sys.stderr, flush=True)
+        del sets
+        torch.cuda.empty_cache()
+    if raw_path:
+        np.savez(raw_path, **{n.split()[0].replace("/", "_"): a for n, a in raw.items()})
     return out
 
 

@@ -212,3 +212,17 @@ def test_inv_freq_rejects_bad_head_dim(fence):
     buf = (ctypes.c_float * 256)()
     assert _raw("fence_rope_inv_freq")(ctypes.cast(buf, ctypes.c_void_p), 127, 1e6) == EINVAL
     assert _raw("fence_rope_inv_freq")(None, 128, 1e6) == EINVAL
+
+
+def test_wave_clock_only_in_the_instrumented_library(fence):
+    """include/fence/wave_clock.h's entry points exist in
+    libfence_ops_waveclock.so (gemv_q6k.hip built with FENCE_WAVE_CLOCK=1) and
+    not in the product library, whose kernels carry no instrumentation."""
+    decls = header_declarations(os.path.join(ROOT, "include", "fence", "wave_clock.h"))
+    assert decls == {"fence_wave_clock_clear": 0, "fence_wave_clock_read": 2}
+    wc = ctypes.CDLL(os.path.join(os.path.dirname(fence_ops.LIB_PATH), "libfence_ops_waveclock.so"))
+    for name in decls:
+        assert hasattr(wc, name), f"{name} missing from the instrumented library"
+        assert not hasattr(fence.lib(), name), f"{name} exported by the product library"
+    for name in header_declarations():  # the same C ABI otherwise
+        assert hasattr(wc, name), name
