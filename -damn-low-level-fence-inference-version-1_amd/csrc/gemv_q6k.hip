@@ -167,14 +167,23 @@ __device__ __forceinline__ float q6_col_bias(uint32_t x01, uint32_t x23) {
 // d * acc is rounded on its own and never fused into the caller's sum, so
 // every kernel layout that adds the same lane values in the same order gets
 // the same bits.
+// a . b + c in the three-operand v_dot2_f32_f16.  The builtin's form is
+// shrunk to the two-operand v_dot2c_f32_f16 (d += a . b) wherever it can be,
+// which for a chain starting from a loop-invariant c costs a v_mov copy of c
+// first; this keeps c where it is.  Same instruction arithmetic, same bits.
+__device__ __forceinline__ float dot2_f16(h2 a, h2 b, float c) {
+    float d;
+    asm("v_dot2_f32_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
 __device__ __forceinline__ float q6_lane_dot(const Q6Lane& q, const uint32_t* xh, const float* kb, const int* sc,
                                              float d) {
 #pragma clang fp contract(off)
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        float p = __builtin_amdgcn_fdot2(q6_pair(q.w[c], 0x00050004u), __builtin_bit_cast(h2, xh[2 * c]), kb[c],
-                                         false);
+        float p = dot2_f16(q6_pair(q.w[c], 0x00050004u), __builtin_bit_cast(h2, xh[2 * c]), kb[c]);
         p = __builtin_amdgcn_fdot2(q6_pair(q.w[c], 0x00070006u), __builtin_bit_cast(h2, xh[2 * c + 1]), p, false);
         acc = __builtin_fmaf(static_cast<float>(sc[c]), p, acc);
     }
@@ -307,9 +316,12 @@ constexpr int staged_waves() { return NORM && !PAIR && WPR == 1 ? 8 : (PAIR && W
 // 400, in-process A/B: the o projection 2560 x 4096 4.92 -> 4.60 us, Llama-3-8B
 // 4096 x 4096 6.44 -> 5.80 us; the same prefetch in the other layouts cost
 // more registers than it saved (gate/up pair, 9728 x 2560) or changed nothing.
+// VW (NORM launches): the norm's 64-lane virtual waves each wave holds,
+// ceil((T / 64) / NW), chosen at launch so no slot is always empty (a slot
+// costs its loads, masks and reductions whether or not it is used).
 // CLOCK: the instrumented copy (FENCE_WAVE_CLOCK builds launch it on the grid
 // the plain kernel gets); every product launch has CLOCK = false.
-template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false, bool CLOCK = false>
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false, bool CLOCK = false, int VW = 0>
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
     static_assert(!XW || (PASSES * WPR == 4 && !PAIR && NORM == 0), "XW: four passes, plain rows");
@@ -357,7 +369,8 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
     // Every load is unconditional (clamped slots, and hidden again in place of
     // an absent residual), so all are in flight together and none waits for
     // the blocks issued after them.
-    constexpr int kVW = NORM ? (16 + NW - 1) / NW : 1;
+    static_assert(NORM == 0 || (VW >= 1 && VW * NW <= 16 + NW - 1), "VW: 1 .. ceil(16 / NW) slots");
+    constexpr int kVW = NORM ? VW : 1;
     constexpr int kVpt = NORM ? NORM : 1;
     f4 nh[kVW][kVpt], nr[kVW][kVpt], nw[kVW][kVpt];
     auto norm_slot = [&](int i, int jj, int* f) {
@@ -737,14 +750,31 @@ int launch_grid(Kernel kernel, int threads, std::atomic<int>* cache, int64_t gro
     return launch_grid_as(kernel, kernel, threads, cache, groups, s, args...);
 }
 
-template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
-int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW, int VW>
+int launch_staged_vw(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
     static std::atomic<int> cache[64];
     constexpr int nw = staged_waves<WPR, PAIR, NORM>();
     constexpr int out_per_group = PAIR ? nw / WPR / 2 : nw / WPR;
-    return launch_grid_as(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW, false>,
-                          gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW, FENCE_WAVE_CLOCK != 0>,
+    return launch_grid_as(gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW, false, VW>,
+                          gemv_q6k_staged_kernel<PASSES, WPR, PAIR, MULTI, NORM, XW, FENCE_WAVE_CLOCK != 0, VW>,
                           kWave * nw, cache, (n_out + out_per_group - 1) / out_per_group, s, job, x, nb, rin);
+}
+
+template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false>
+int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
+    if constexpr (NORM == 0) {
+        return launch_staged_vw<PASSES, WPR, PAIR, MULTI, NORM, XW, 0>(job, n_out, x, nb, rin, s);
+    } else {
+        constexpr int nw = staged_waves<WPR, PAIR, NORM>();
+        const int vw = (rin.T / kWave + nw - 1) / nw;  // rin.T <= 1024: at most 16 / nw
+        if (vw <= 1) return launch_staged_vw<PASSES, WPR, PAIR, MULTI, NORM, XW, 1>(job, n_out, x, nb, rin, s);
+        if (vw == 2 || nw == 8) return launch_staged_vw<PASSES, WPR, PAIR, MULTI, NORM, XW, 2>(job, n_out, x, nb, rin, s);
+        if constexpr (nw == 4) {
+            if (vw == 3) return launch_staged_vw<PASSES, WPR, PAIR, MULTI, NORM, XW, 3>(job, n_out, x, nb, rin, s);
+            return launch_staged_vw<PASSES, WPR, PAIR, MULTI, NORM, XW, 4>(job, n_out, x, nb, rin, s);
+        }
+        return FENCE_ERROR_INVALID_VALUE;  // not reached: nw is 4 or 8
+    }
 }
 
 // The staged kernel for a row of nb blocks, at q6_wpr / q6_passes.  Only the
