@@ -287,17 +287,19 @@ __device__ __forceinline__ int mat_of(const Q6Job& job, int64_t r, int64_t* lr) 
 }
 
 // Waves of a staged workgroup: 4; 8 for a gate/up pair whose rows take four
-// waves each; 8 for a multi launch that normalises its input row in the
-// prologue with one wave per row.  Measured on MI355X for the last: every
-// workgroup computes the row norm, and two 8-wave workgroups per CU instead
-// of five 4-wave ones cut q/k/v from 9.04 to 7.28 us (K = 2560) and from
-// 10.44 to 9.40 us (K = 4096), p50; 6-, 10- and 12-wave workgroups were
-// slower (a workgroup's waves spread over the CU's four SIMDs, so only
-// multiples of four fill it), and so was 8 for the gate/up pair (15.24 ->
-// 16.04 us).  A row's arithmetic does not depend on the workgroup, so every
-// result is the same.
+// waves each; 8 for a launch that normalises its input row in the prologue
+// with one wave per row (every workgroup computes the row norm, so wider
+// workgroups compute it fewer times per CU).  Measured on MI355X: two 8-wave
+// workgroups per CU instead of five 4-wave ones cut q/k/v from 9.04 to
+// 7.28 us (K = 2560) and from 10.44 to 9.40 us (K = 4096), p50; 6-, 10- and
+// 12-wave workgroups were slower (a workgroup's waves spread over the CU's
+// four SIMDs, so only multiples of four fill it).  The gate/up pair with its
+// norm runs at 6 waves per SIMD (80 VGPRs), three 8-wave workgroups per CU:
+// Qwen3-4B decode steps 1,718 -> 1,710 us per token against six 4-wave ones
+// (bench.py --decode-only, interleaved runs).  A row's arithmetic does not
+// depend on the workgroup, so every result is the same.
 template <int WPR, bool PAIR, int NORM = 0>
-constexpr int staged_waves() { return NORM && !PAIR && WPR == 1 ? 8 : (PAIR && WPR == 4 ? 8 : 4); }
+constexpr int staged_waves() { return NORM && WPR == 1 ? 8 : (PAIR && WPR == 4 ? 8 : 4); }
 
 // Staged kernel.  WPR waves per row (1, 2 or 4), each over at most 4 * PASSES
 // <= 16 blocks.  LDS: one buffer of kSegBytes per wave + red[].  A workgroup
