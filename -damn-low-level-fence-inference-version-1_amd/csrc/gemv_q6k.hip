@@ -58,6 +58,16 @@
 #ifndef FENCE_GEMV_Q6K_BALANCED
 #define FENCE_GEMV_Q6K_BALANCED 0
 #endif
+// 1: rows of 33-40 blocks take two waves of up to five passes (20 block
+// slots for 17-20 blocks) instead of four waves of three passes (12 slots for
+// 8-10 blocks, the rest masked); 0 (kept): four waves.  The wider form issues
+// 22% fewer loop instructions per row but needs 111 VGPRs (4 waves per SIMD
+// against 7): Qwen3-4B decode steps 1,722-1,724 us per token against 1,713
+// (bench.py --decode-only against a `make TAG=nowide
+// EXTRA=-DFENCE_GEMV_Q6K_WIDE=0` build, interleaved runs on one box).
+#ifndef FENCE_GEMV_Q6K_WIDE
+#define FENCE_GEMV_Q6K_WIDE 0
+#endif
 // Launches of at most this many rows of 13-16 blocks take the one-wave layout
 // spread over four waves per row (XW below; same results, bit for bit).
 // Measured on MI355X, p50: the 2560 x 4096 o projection runs in 4.96 us with
@@ -210,7 +220,7 @@ __host__ __device__ constexpr int q6_wpr(int nb) {
     return nb > 4 * kMaxSegBlocks        ? 1
            : FENCE_GEMV_Q6K_SPLIT == 2 ? (nb <= 4 ? 1 : nb <= 8 ? 2 : 4)
            : FENCE_GEMV_Q6K_SPLIT == 1 ? (nb <= 8 ? 1 : nb <= 16 ? 2 : 4)
-                                       : (nb <= 16 ? 1 : nb <= 32 ? 2 : 4);
+                                       : (nb <= 16 ? 1 : nb <= (FENCE_GEMV_Q6K_WIDE ? 40 : 32) ? 2 : 4);
 }
 __host__ __device__ constexpr int q6_passes(int nb) { return (nb + 4 * q6_wpr(nb) - 1) / (4 * q6_wpr(nb)); }
 
@@ -798,6 +808,9 @@ int launch_nb(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const 
     }
     if constexpr (NORM == 0) {
         FENCE_Q6_STAGED(3, 4) FENCE_Q6_STAGED(4, 4)
+        if constexpr (FENCE_GEMV_Q6K_SPLIT == 0 && FENCE_GEMV_Q6K_WIDE) {
+            FENCE_Q6_STAGED(5, 2)
+        }
     }
 #undef FENCE_Q6_STAGED
     return FENCE_ERROR_INVALID_VALUE;  // a pair the table cannot produce
