@@ -456,7 +456,10 @@ int check_mode() {
 
 // ------------------------------------------------------------ time mode
 
-int time_mode(int n_layers, int pos, bool with_graph) {
+// reps: timed tokens of each sequence (after 3 warm-up tokens);
+// fused_only: skip the reference launch order (about 4x the dispatches of
+// the fused one), for profiler passes that serialise every dispatch.
+int time_mode(int n_layers, int pos, bool with_graph, int reps, bool fused_only) {
     std::vector<Layer> layers(n_layers);
     for (int l = 0; l < n_layers; ++l) fill_layer(layers[l], 100 + l);
     uint8_t* table = dalloc<uint8_t>(static_cast<size_t>(V) * (E / 32) * 34);
@@ -499,8 +502,8 @@ int time_mode(int n_layers, int pos, bool with_graph) {
         HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
         return 1e3 * ms / reps;
     };
-    const double us_ref = time_it(token_reference, 3, 10);
-    const double us_fused = time_it(token_fused, 3, 10);
+    const double us_ref = fused_only ? 0.0 : time_it(token_reference, 3, reps);
+    const double us_fused = time_it(token_fused, 3, reps);
     // (c) one token of (b) captured as a graph (its memset becomes a copy from
     // a zeroed buffer)
     hipGraph_t graph = nullptr;
@@ -519,7 +522,7 @@ int time_mode(int n_layers, int pos, bool with_graph) {
     fence_argmax_ws(s.logits, s.argmax_out, V, s.score_buf, 16 * int64_t(NQ) * CTX, st);
     HIP_CHECK(hipStreamEndCapture(st, &graph));
     HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
-    us_graph = time_it([&](int) { HIP_CHECK(hipGraphLaunch(exec, st)); }, 3, 10);
+    us_graph = time_it([&](int) { HIP_CHECK(hipGraphLaunch(exec, st)); }, 3, reps);
     }
 
     const double weight_bytes = n_layers * (double)(q6_bytes(QD, E) + 2 * q6_bytes(KVD, E) + q6_bytes(E, QD) +
@@ -544,14 +547,25 @@ int time_mode(int n_layers, int pos, bool with_graph) {
 
 int main(int argc, char** argv) {
     if (argc >= 2 && std::string(argv[1]) == "--time") {
-        const int layers = argc >= 3 ? std::atoi(argv[2]) : 36;
-        const int pos = argc >= 4 ? std::atoi(argv[3]) : 2915;
-        const bool graph = !(argc >= 5 && std::string(argv[4]) == "--no-graph");
-        if (layers < 1 || layers > 64 || pos < 0 || pos >= CTX) {
-            std::fprintf(stderr, "usage: decode_step [--time [layers 1..64] [pos 0..%d] [--no-graph]]\n", CTX - 1);
+        // --time [layers] [pos] [--no-graph] [--fused-only] [--tokens N]
+        int layers = 36, pos = 2915, reps = 10, npos = 0;
+        bool graph = true, fused_only = false, bad = false;
+        for (int i = 2; i < argc; ++i) {
+            const std::string a = argv[i];
+            if (a == "--no-graph") graph = false;
+            else if (a == "--fused-only") fused_only = true;
+            else if (a == "--tokens" && i + 1 < argc) reps = std::atoi(argv[++i]);
+            else if (npos == 0 && !a.empty() && a[0] != '-') layers = std::atoi(argv[i]), ++npos;
+            else if (npos == 1 && !a.empty() && a[0] != '-') pos = std::atoi(argv[i]), ++npos;
+            else bad = true;
+        }
+        if (bad || layers < 1 || layers > 64 || pos < 0 || pos >= CTX || reps < 1 || reps > 1000) {
+            std::fprintf(stderr,
+                         "usage: decode_step [--time [layers 1..64] [pos 0..%d] [--no-graph] [--fused-only] "
+                         "[--tokens 1..1000]]\n", CTX - 1);
             return 2;
         }
-        return time_mode(layers, pos, graph);
+        return time_mode(layers, pos, graph, reps, fused_only);
     }
     return check_mode();
 }

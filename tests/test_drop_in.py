@@ -49,3 +49,21 @@ def test_drop_in_decode_step_timing():
     assert rec["layers"] == 2 and rec["pos"] == 300
     for k in ("us_per_token_reference_sequence", "us_per_token_fused", "us_per_token_fused_graph"):
         assert rec[k] > 0
+
+
+@pytest.mark.gpu
+def test_drop_in_decode_step_fused_only_timing():
+    """The profiler form: the fused sequence alone, two timed tokens."""
+    line = run([STEP, "--time", "2", "300", "--no-graph", "--fused-only", "--tokens", "2"]).strip().splitlines()[-1]
+    rec = json.loads(line)
+    assert rec["us_per_token_fused"] > 0 and rec["us_per_token_reference_sequence"] == 0
+
+
+def test_drop_in_decode_step_rejects_bad_options():
+    """Argument errors end before any device call (runs without a GPU)."""
+    import subprocess
+    if not os.path.exists(STEP):
+        pytest.skip("decode_step is not built")
+    for args in (["--bogus"], ["--tokens", "0"], ["70"], ["2", "5000"]):
+        r = subprocess.run([STEP, "--time"] + args, capture_output=True, text=True, timeout=60)
+        assert r.returncode == 2 and "usage" in r.stderr, args
