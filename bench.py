@@ -610,6 +610,9 @@ def measure_configs(torch, F, reps, extended, back_to_back_timing=True):
         r = summarize([hev.elapsed_ms(a, b) * 1e3 for a, b in evs], nbytes, kernel)
         hev.destroy_all()
         r = {"config": cfg, "key": key, "op": name, **r, "launches_per_call": launches, "sets": len(sets),
+             # this library's kernel dispatches of the op, in launch order: the untimed calls, then
+             # the timed ones (a profile of the run is matched to ops by this count)
+             "dispatches": (max(3, len(sets)) + reps) * launches,
              "cold": "warm (one set)" if warm else ("1 GiB scrub between launches" if small else
                                                     "rotating buffer sets")}
         if note:
