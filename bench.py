@@ -1031,6 +1031,17 @@ def decode_op_set(torch, F, gen, reps):
     e1.record(s)
     torch.cuda.synchronize()
     out["sustained_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+    # the same reps op sets queued behind a spin kernel: GPU time only
+    torch.cuda._sleep(200_000_000)  # ~0.1 s: longer than queueing 6 x reps launches
+    e0.record(s)
+    h0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    qms = (time.perf_counter() - h0) * 1e3
+    e1.record(s)
+    torch.cuda.synchronize()
+    out["queued_sustained_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+    out["queued_sustained_host_queue_ms"] = round(qms, 2)
 
     # the same sequence captured once in a HIP graph and replayed
     try:
@@ -1059,6 +1070,43 @@ def decode_op_set(torch, F, gen, reps):
         e1.record(s)
         torch.cuda.synchronize()
         out["graph_sustained_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+        # the same op set ten times in one graph: separates a per-replay cost (graph launch) from a
+        # per-node one (a node of a replayed graph costing more than an eager launch)
+        g10 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g10):
+            sh_cap = torch.cuda.current_stream().cuda_stream
+            for _ in range(10):
+                F.embed_q8_0(hidden.data_ptr(), table.data_ptr(), tok, L3_HIDDEN, sh_cap)
+                F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w1.data_ptr(), L3_HIDDEN, 1e-5, sh_cap)
+                F.rope(q.data_ptr(), k.data_ptr(), 1, NQ, NKV, HD, None, pos, L3_THETA, F.ROPE_INTERLEAVED, sh_cap)
+                F.softmax_rows(scores.data_ptr(), NQ, pos + 1, max_ctx, sh_cap)
+                F.rms_norm(normed.data_ptr(), hidden.data_ptr(), w2.data_ptr(), L3_HIDDEN, 1e-5, sh_cap)
+                F.silu_elementwise_mul(act.data_ptr(), gate.data_ptr(), up.data_ptr(), L3_FFN, sh_cap)
+        for _ in range(3):
+            g10.replay()
+        torch.cuda.synchronize()
+        n10 = max(1, reps // 10)
+        e0.record(s)
+        for _ in range(n10):
+            g10.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+        out["graph_x10_sustained_us"] = round(e0.elapsed_time(e1) * 1e3 / (10 * n10), 2)
+        # replays queued behind a spin kernel: GPU time only, whatever the host's launch rate
+        for name, graph, per, n in (("graph_queued_us", g, 1, reps), ("graph_x10_queued_us", g10, 10, n10)):
+            torch.cuda.synchronize()
+            torch.cuda._sleep(200_000_000)  # ~0.1 s: longer than queueing the replays
+            e0.record(s)
+            h0 = time.perf_counter()
+            for _ in range(n):
+                graph.replay()
+            qms = (time.perf_counter() - h0) * 1e3
+            e1.record(s)
+            torch.cuda.synchronize()
+            out[name] = round(e0.elapsed_time(e1) * 1e3 / (per * n), 2)
+            out[name.replace("_us", "_host_queue_ms")] = round(qms, 2)
+        out["graph_note"] = ("graph_sustained_us: one op set per graph, replays back to back; graph_x10_sustained_us: "
+                             "ten op sets per graph (60 nodes), per op set")
     except Exception as exc:  # graph capture is optional for the report
         out["graph_error"] = str(exc)[:200]
     return out
