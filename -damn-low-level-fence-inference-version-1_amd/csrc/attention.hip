@@ -30,6 +30,21 @@
 #ifndef FENCE_ATTN_TARGET_WG
 #define FENCE_ATTN_TARGET_WG 1024
 #endif
+// 1: fence_gqa_attention_qk_f16_arrive merges in the split launch (one
+// launch); 0: it launches the merge kernel as fence_gqa_attention_qk_f16 does
+// (an A/B build: `make TAG=noarrive EXTRA=-DFENCE_ATTN_ARRIVE=0`).  Results
+// are the same bits either way.
+#ifndef FENCE_ATTN_ARRIVE
+#define FENCE_ATTN_ARRIVE 1
+#endif
+// Words between two arrival counters (at most FENCE_ARRIVE_WORDS_PER_HEAD):
+// every counter on a cache line of its own, so the device-scope atomics of
+// different head groups do not queue behind one another.
+#ifndef FENCE_ATTN_ARRIVE_STRIDE
+#define FENCE_ATTN_ARRIVE_STRIDE 64
+#endif
+static_assert(FENCE_ATTN_ARRIVE_STRIDE >= 1 && FENCE_ATTN_ARRIVE_STRIDE <= FENCE_ARRIVE_WORDS_PER_HEAD,
+              "arrival counter stride");
 
 namespace fence {
 namespace {
@@ -64,6 +79,37 @@ struct QkIn {
     InvFreq tab;
 };
 
+// One wave's share of the merge of one query head over splits <= kWave:
+// output dim d, lane = d mod 64.  ld(i) reads float i of the head's partials
+// [splits][HD + 2].  Shared by the merge kernel and the split kernel's
+// last-arrival merge, so both give the same bits.
+template <class Load>
+__device__ __forceinline__ float merge_splits_small(Load ld, int splits, int d, int lane) {
+    constexpr int kRow = 128 + 2;
+    const int sl = lane < splits ? lane : 0;  // clamped: a valid split, dropped below
+    uint32_t ml = static_cast<uint32_t>(sl * kRow);
+    asm volatile("" : "+v"(ml));
+    const float m_l = ld(ml);
+    const float l_l = ld(ml + 1);
+    float os[kWave];
+#pragma unroll
+    for (int b = 0; b < kWave; ++b) {
+        uint32_t ob = static_cast<uint32_t>((b < splits ? b : 0) * kRow + 2 + d);
+        asm volatile("" : "+v"(ob));
+        os[b] = ld(ob);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const bool on = lane < splits;
+    const float M = wave_reduce(on ? m_l : -__builtin_inff(), OpMax{});
+    const float c_l = (!on || l_l == 0.0f) ? 0.0f : exp2_hw(m_l - M);  // an empty split weighs 0
+    const float L = wave_reduce(on ? l_l * c_l : 0.0f, OpAdd{});
+    float O = 0.0f;
+#pragma unroll
+    for (int b = 0; b < kWave; ++b)
+        if (b < splits) O = __builtin_fmaf(readlane(c_l, b), os[b], O);
+    return L == 0.0f ? 0.0f : O / L;
+}
+
 // Split kernel: grid (n_kv * head_groups, splits); HD = 128.  The workgroup
 // walks its positions in sub-chunks of kSub (= 64): (A) every 16-lane group
 // scores its positions for the GT heads into LDS, (B) every wave takes each
@@ -80,13 +126,22 @@ struct QkIn {
 // there (the cache row is never read), and the first head group's one writes
 // the row to the caches.  The first sub-chunk's K and V loads are issued
 // before the prologue, which runs while they are in flight.
-template <int GT, bool FINAL, int ROPE>
+// ARRIVE (with !FINAL, at most kWave splits): no merge launch.  The partials
+// are written with device-coherent stores (agent-scope atomic stores, which
+// write through the XCD's L2); once they have completed, the workgroup bumps
+// arrive[its (kv head, head group)], and the workgroup that brings it to
+// `splits` -- the last of that head group's splits -- resets it to 0 and
+// merges the group's heads itself, reading every split's partials with
+// device-coherent loads, in the merge kernel's arithmetic.  No workgroup ever
+// waits for another.
+template <int GT, bool FINAL, int ROPE, bool ARRIVE = false>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict__ out, uint16_t* __restrict__ out16,
                                                               float* __restrict__ ws,
                                                               const float* __restrict__ q,
                                                               const uint16_t* __restrict__ kc,
                                                               const uint16_t* __restrict__ vc, int n_q, int n_kv,
-                                                              int seq_len, int chunk, float scale2, const QkIn qk) {
+                                                              int seq_len, int chunk, float scale2, const QkIn qk,
+                                                              uint32_t* __restrict__ arrive) {
     constexpr int HD = 128;
     constexpr int HALF = HD / 2;
     constexpr int G = HD / 8;              // prologue lanes (units) per head
@@ -348,11 +403,47 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         } else {
             // partial of (head h, split): [m, l, o[HD]]
             float* p = ws + (static_cast<int64_t>(h) * gridDim.y + split) * (HD + 2);
-            if (d == 0) {
-                p[0] = mg;
-                p[1] = l;
+            if constexpr (ARRIVE) {
+                if (d == 0) {
+                    __hip_atomic_store(p, mg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(p + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __hip_atomic_store(p + 2 + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                if (d == 0) {
+                    p[0] = mg;
+                    p[1] = l;
+                }
+                p[2 + d] = acc;
             }
-            p[2 + d] = acc;
+        }
+    }
+    if constexpr (!FINAL && ARRIVE) {
+        __shared__ uint32_t last;
+        // Every wave's partial stores have completed (gfx9 counts stores in
+        // vmcnt) before the one arrival below is made.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t before = __hip_atomic_fetch_add(arrive + bx * FENCE_ATTN_ARRIVE_STRIDE, 1u, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+            last = before + 1 == gridDim.y ? 1u : 0u;
+        }
+        __syncthreads();
+        if (last == 0) return;  // workgroup-uniform
+        if (threadIdx.x == 0)
+            __hip_atomic_store(arrive + bx * FENCE_ATTN_ARRIVE_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // The merge of heads h0 .. h0 + ng - 1: wave w takes head-halves
+        // e = w, w + 4, ..: head e / 2, dims 64 (e % 2) + lane.
+        const int splits = static_cast<int>(gridDim.y);
+        for (int e = wave; e < 2 * ng; e += kThreads / kWave) {
+            const int h = h0 + e / 2, d = (e % 2) * kWave + lane;
+            const float* p = ws + static_cast<int64_t>(h) * splits * (HD + 2);
+            const float r = merge_splits_small(
+                [p](uint32_t i) { return __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
+                splits, d, lane);
+            if (out) out[static_cast<int64_t>(h) * HD + d] = r;
+            if (out16) out16[static_cast<int64_t>(h) * HD + d] = f32_to_f16_bits(r);
         }
     }
 }
@@ -375,28 +466,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(float* __restrict__ out
     const float* p = ws + static_cast<int64_t>(h) * splits * kRow;
     float r;
     if (splits <= kWave) {
-        const int sl = lane < splits ? lane : 0;  // clamped: a valid split, dropped below
-        uint32_t ml = static_cast<uint32_t>(sl * kRow);
-        asm volatile("" : "+v"(ml));
-        const float m_l = p[ml];
-        const float l_l = p[ml + 1];
-        float os[kWave];
-#pragma unroll
-        for (int b = 0; b < kWave; ++b) {
-            uint32_t ob = static_cast<uint32_t>((b < splits ? b : 0) * kRow + 2 + d);
-            asm volatile("" : "+v"(ob));
-            os[b] = p[ob];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const bool on = lane < splits;
-        const float M = wave_reduce(on ? m_l : -__builtin_inff(), OpMax{});
-        const float c_l = (!on || l_l == 0.0f) ? 0.0f : exp2_hw(m_l - M);  // an empty split weighs 0
-        const float L = wave_reduce(on ? l_l * c_l : 0.0f, OpAdd{});
-        float O = 0.0f;
-#pragma unroll
-        for (int b = 0; b < kWave; ++b)
-            if (b < splits) O = __builtin_fmaf(readlane(c_l, b), os[b], O);
-        r = L == 0.0f ? 0.0f : O / L;
+        r = merge_splits_small([p](uint32_t i) { return p[i]; }, splits, d, lane);
     } else {
         __shared__ float cw[kMaxMergeSplits];
         __shared__ float red[2];
@@ -490,7 +560,7 @@ __global__ __launch_bounds__(256) void store_kv_kernel(uint16_t* __restrict__ kc
 
 template <int GT, int ROPE>
 int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc, int n_q, int n_kv,
-                 int seq_len, int64_t ws_floats, float scale, const QkIn& qk, hipStream_t s) {
+                 int seq_len, int64_t ws_floats, float scale, const QkIn& qk, uint32_t* arrive, hipStream_t s) {
     constexpr int HD = 128;
     const int group = n_q / n_kv;
     const int head_groups = (group + GT - 1) / GT;
@@ -507,11 +577,15 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
     if (splits > kMaxMergeSplits) splits = kMaxMergeSplits;
     const int chunk = static_cast<int>((seq_len + splits - 1) / splits);
     const dim3 grid(static_cast<unsigned>(base_wg), static_cast<unsigned>(splits));
+    uint32_t* const no_arrive = nullptr;
     if (splits == 1)
         return launch(attn_split_kernel<GT, true, ROPE>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc, n_q,
-                      n_kv, seq_len, chunk, scale, qk);
+                      n_kv, seq_len, chunk, scale, qk, no_arrive);
+    if (FENCE_ATTN_ARRIVE && arrive && splits <= kWave)  // the last arrival of each head group merges it
+        return launch(attn_split_kernel<GT, false, ROPE, true>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc,
+                      vc, n_q, n_kv, seq_len, chunk, scale, qk, arrive);
     if (int st = launch(attn_split_kernel<GT, false, ROPE>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc,
-                        n_q, n_kv, seq_len, chunk, scale, qk))
+                        n_q, n_kv, seq_len, chunk, scale, qk, no_arrive))
         return st;
     return launch(attn_merge_kernel, dim3(static_cast<unsigned>(n_q)), dim3(HD), 0, s, out, out16, ws,
                   static_cast<int>(splits));
@@ -522,12 +596,15 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
 template <int GT>
 int launch_split_qk(float* out, uint16_t* out16, float* ws, const float* q, const uint16_t* kc, const uint16_t* vc,
                     int n_q, int n_kv, int seq_len, int64_t ws_floats, float scale, const QkIn* qk, int rope,
-                    hipStream_t s) {
+                    uint32_t* arrive, hipStream_t s) {
     if (!qk)
-        return launch_split<GT, kRopeNone>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, QkIn{}, s);
+        return launch_split<GT, kRopeNone>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, QkIn{},
+                                           arrive, s);
     if (rope == kRopeNeox)
-        return launch_split<GT, kRopeNeox>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, *qk, s);
-    return launch_split<GT, kRopeInter>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, *qk, s);
+        return launch_split<GT, kRopeNeox>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, *qk,
+                                           arrive, s);
+    return launch_split<GT, kRopeInter>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale, *qk, arrive,
+                                        s);
 }
 
 }  // namespace
@@ -537,10 +614,12 @@ int launch_split_qk(float* out, uint16_t* out16, float* ws, const float* q, cons
 // ws holds ws_floats floats (the reference's score_buf: n_q * max_ctx).
 // qk (with style rope): q is unprepared and the launch applies QK-norm, RoPE
 // and the KV store of position seq_len - 1 itself; only on the vector path
-// (the caller checks vec_attention).
+// (the caller checks vec_attention).  arrive (n_q * FENCE_ARRIVE_WORDS_PER_HEAD
+// zeroed words, left zeroed): a split launch of at most 64 splits merges them
+// itself.
 int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void* kcv, const void* vcv, int hd,
                          int n_q, int n_kv, int seq_len, int max_ctx, float* ws, int64_t ws_floats, hipStream_t s,
-                         const QkIn* qk = nullptr, int rope = kRopeNone) {
+                         const QkIn* qk = nullptr, int rope = kRopeNone, uint32_t* arrive = nullptr) {
     if ((!out && !out16) || !q || !kcv || !vcv || hd <= 0 || n_q <= 0 || n_kv <= 0 || (n_q % n_kv) != 0)
         return FENCE_ERROR_INVALID_VALUE;
     if (out16 && !aligned(out16, 2)) return FENCE_ERROR_INVALID_VALUE;
@@ -556,17 +635,23 @@ int gqa_attention_launch(float* out, uint16_t* out16, const float* q, const void
     if (qk && !vec) return FENCE_ERROR_INVALID_VALUE;
     if (vec) {
         if (FENCE_ATTN_GT_MAX == 1)
-            return launch_split_qk<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+            return launch_split_qk<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk,
+                                      rope, arrive, s);
         if (FENCE_ATTN_GT_MAX == 2 && group >= 2)
-            return launch_split_qk<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+            return launch_split_qk<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk,
+                                      rope, arrive, s);
         if (group >= 4)
-            return launch_split_qk<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+            return launch_split_qk<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk,
+                                      rope, arrive, s);
         if (group == 2)
-            return launch_split_qk<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+            return launch_split_qk<2>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk,
+                                      rope, arrive, s);
         if (group == 1)
-            return launch_split_qk<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+            return launch_split_qk<1>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk,
+                                      rope, arrive, s);
         // group 3: masked
-        return launch_split_qk<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk, rope, s);
+        return launch_split_qk<4>(out, out16, ws, q, kc, vc, n_q, n_kv, seq_len, ws_floats, scale2, qk,
+                                  rope, arrive, s);
     }
     // the generic path keeps scores in score_buf, n_q rows of max_ctx
     if (!ws || ws_floats < static_cast<int64_t>(n_q) * max_ctx) return FENCE_ERROR_INVALID_VALUE;
@@ -609,11 +694,13 @@ extern "C" int fence_gqa_attention_f16(float* attn_out, void* out_f16, const flo
                                        n_q_heads, n_kv_heads, seq_len, max_ctx, score_buf, score_buf_floats, stream);
 }
 
-extern "C" int fence_gqa_attention_qk_f16(float* attn_out, void* out_f16, float* q, float* k, const float* v,
-                                          const float* q_norm_w, const float* k_norm_w, void* k_cache, void* v_cache,
-                                          int head_dim, int n_q_heads, int n_kv_heads, int pos, int max_ctx, float eps,
-                                          float freq_base, int style, float* score_buf, int64_t score_buf_floats,
-                                          hipStream_t stream) {
+namespace {
+
+// fence_gqa_attention_qk_f16, and with arrive its one-launch form.
+int attention_qk_f16(float* attn_out, void* out_f16, float* q, float* k, const float* v, const float* q_norm_w,
+                     const float* k_norm_w, void* k_cache, void* v_cache, int head_dim, int n_q_heads, int n_kv_heads,
+                     int pos, int max_ctx, float eps, float freq_base, int style, float* score_buf,
+                     int64_t score_buf_floats, uint32_t* arrive, hipStream_t stream) {
     using namespace fence;
     if (!out_f16 || !q || !k || !v || !k_cache || !v_cache || score_buf_floats < 0) return FENCE_ERROR_INVALID_VALUE;
     if (pos < 0 || max_ctx < 1 || pos >= max_ctx || n_q_heads <= 0 || n_kv_heads <= 0) return FENCE_ERROR_INVALID_VALUE;
@@ -652,7 +739,30 @@ extern "C" int fence_gqa_attention_qk_f16(float* attn_out, void* out_f16, float*
     qk.eps = eps;
     rope_inv_freq_host(qk.tab.v, head_dim, freq_base);
     return gqa_attention_launch(attn_out, o16, q, k_cache, v_cache, head_dim, n_q_heads, n_kv_heads, pos + 1, max_ctx,
-                                score_buf, score_buf_floats, stream, &qk, style);
+                                score_buf, score_buf_floats, stream, &qk, style, arrive);
+}
+
+}  // namespace
+
+extern "C" int fence_gqa_attention_qk_f16(float* attn_out, void* out_f16, float* q, float* k, const float* v,
+                                          const float* q_norm_w, const float* k_norm_w, void* k_cache, void* v_cache,
+                                          int head_dim, int n_q_heads, int n_kv_heads, int pos, int max_ctx, float eps,
+                                          float freq_base, int style, float* score_buf, int64_t score_buf_floats,
+                                          hipStream_t stream) {
+    return attention_qk_f16(attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, head_dim, n_q_heads,
+                            n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf, score_buf_floats, nullptr,
+                            stream);
+}
+
+extern "C" int fence_gqa_attention_qk_f16_arrive(float* attn_out, void* out_f16, float* q, float* k, const float* v,
+                                                 const float* q_norm_w, const float* k_norm_w, void* k_cache,
+                                                 void* v_cache, int head_dim, int n_q_heads, int n_kv_heads, int pos,
+                                                 int max_ctx, float eps, float freq_base, int style, float* score_buf,
+                                                 int64_t score_buf_floats, uint32_t* arrive, hipStream_t stream) {
+    if (!arrive || !fence::aligned(arrive, 4)) return FENCE_ERROR_INVALID_VALUE;
+    return attention_qk_f16(attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, head_dim, n_q_heads,
+                            n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf, score_buf_floats, arrive,
+                            stream);
 }
 
 extern "C" int fence_store_kv(void* k_cache, void* v_cache, const float* k, const float* v, int pos, int kv_dim,

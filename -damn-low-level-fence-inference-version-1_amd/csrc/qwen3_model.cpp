@@ -318,6 +318,7 @@ bool Qwen3Model::load(const std::string& gguf_path, int max_ctx, hipStream_t str
     size_t total = 0;
     for (size_t n : f32_sizes) total += align_up(n * 4, kAlign);
     total += align_up(half_n * 2, kAlign) + align_up(FF * 2, kAlign) + kAlign;
+    total += align_up(size_t(c.n_heads) * FENCE_ARRIVE_WORDS_PER_HEAD * 4, kAlign);
     if (hipMalloc(&scratch_arena_, total) != hipSuccess || hipHostMalloc(&host_token_, sizeof(int)) != hipSuccess) {
         unload();
         return fail("out of memory for scratch buffers", FENCE_ERROR_OUT_OF_MEMORY);
@@ -344,7 +345,10 @@ bool Qwen3Model::load(const std::string& gguf_path, int max_ctx, hipStream_t str
     s.x_half = reinterpret_cast<__half*>(take(half_n * 2));
     s.act_half = reinterpret_cast<__half*>(take(FF * 2));
     s.argmax_out = reinterpret_cast<int*>(take(sizeof(int)));
+    const size_t arrive_bytes = size_t(c.n_heads) * FENCE_ARRIVE_WORDS_PER_HEAD * 4;
+    attn_arrive_ = reinterpret_cast<uint32_t*>(take(arrive_bytes));
     hipError_t e = hipMemsetAsync(kv_arena_, 0, per_cache * 2 * c.n_layers, stream_);
+    if (e == hipSuccess) e = hipMemsetAsync(attn_arrive_, 0, arrive_bytes, stream_);
     if (e == hipSuccess) e = hipStreamSynchronize(stream_);
     if (e != hipSuccess) {
         unload();
@@ -362,6 +366,7 @@ void Qwen3Model::unload() {
     if (own_stream_ && stream_) (void)hipStreamDestroy(stream_);
     weight_arena_ = kv_arena_ = scratch_arena_ = nullptr;
     host_token_ = nullptr;
+    attn_arrive_ = nullptr;
     stream_ = nullptr;
     own_stream_ = false;
     placed_.clear();
@@ -454,11 +459,11 @@ bool Qwen3Model::forward_fused(int token_id, int pos) {
         FENCE_STEP(fence_gemv_q6k_multi_rms(3, w_qkv, y_qkv, b_qkv, m_qkv, &attn_in, E, st));
         if (pending) std::swap(cur, next);
         const bool qk_norm = w.attn_q_norm && w.attn_k_norm;
-        FENCE_STEP(fence_gqa_attention_qk_f16(nullptr, s.x_half, s.q, s.k, s.v, qk_norm ? w.attn_q_norm : nullptr,
-                                              qk_norm ? w.attn_k_norm : nullptr, kv_cache.k[l], kv_cache.v[l],
-                                              c.head_dim, c.n_heads, c.n_kv_heads, pos, c.max_ctx, c.rms_eps,
-                                              c.rope_freq_base, FENCE_ROPE_NEOX, s.score_buf,
-                                              kScoreBufScale * int64_t(c.n_heads) * c.max_ctx, st));
+        FENCE_STEP(fence_gqa_attention_qk_f16_arrive(
+            nullptr, s.x_half, s.q, s.k, s.v, qk_norm ? w.attn_q_norm : nullptr, qk_norm ? w.attn_k_norm : nullptr,
+            kv_cache.k[l], kv_cache.v[l], c.head_dim, c.n_heads, c.n_kv_heads, pos, c.max_ctx, c.rms_eps,
+            c.rope_freq_base, FENCE_ROPE_NEOX, s.score_buf, kScoreBufScale * int64_t(c.n_heads) * c.max_ctx,
+            attn_arrive_, st));
         FENCE_STEP(fence_gemv_q6k(w.attn_output, s.x_half, s.down, E, c.q_dim(), st));
         const fence_rms_input ffn_in{cur, s.down, next, w.ffn_norm, s.x_half, c.rms_eps};
         FENCE_STEP(fence_gemv_q6k_swiglu_rms_f16(w.ffn_gate, w.ffn_up, &ffn_in, s.act_half, nullptr, c.ff_dim, E, st));

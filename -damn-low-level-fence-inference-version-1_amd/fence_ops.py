@@ -22,6 +22,7 @@ EINVAL = 22
 HIP_BASE = 1000
 ROPE_NEOX = 0
 ROPE_INTERLEAVED = 1
+ARRIVE_WORDS_PER_HEAD = 64  # FENCE_ARRIVE_WORDS_PER_HEAD
 QK8_0 = 32
 Q8_0_BLOCK_BYTES = 34
 
@@ -63,6 +64,8 @@ SIGNATURES = {
     "fence_qk_norm_rope_store_kv": (_P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_gqa_attention_qk_f16": (_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _I, _P, _L,
                                    _P),
+    "fence_gqa_attention_qk_f16_arrive": (_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _I, _P,
+                                          _L, _P, _P),
     "fence_rms_norm_rope": (_P, _P, _P, _P, _L, _I, _I, _I, _F, _P, _I, _F, _I, _P),
     "fence_swiglu": (_P, _P, _P, _L, _P),
     "fence_softmax_rows": (_P, _L, _I, _L, _P),
@@ -277,6 +280,14 @@ def gqa_attention_qk_f16(attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache
                          n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf, score_buf_floats=0, stream=None):
     _call("fence_gqa_attention_qk_f16", attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, head_dim,
           n_q_heads, n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf, score_buf_floats, stream)
+
+
+def gqa_attention_qk_f16_arrive(attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache, v_cache, head_dim,
+                                n_q_heads, n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf,
+                                score_buf_floats, arrive, stream=None):
+    _call("fence_gqa_attention_qk_f16_arrive", attn_out, out_f16, q, k, v, q_norm_w, k_norm_w, k_cache, v_cache,
+          head_dim, n_q_heads, n_kv_heads, pos, max_ctx, eps, freq_base, style, score_buf, score_buf_floats, arrive,
+          stream)
 
 
 def rms_norm_rope(out, x, w, k, tokens, n_q_heads, n_kv_heads, head_dim, eps, positions, pos0,

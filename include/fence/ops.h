@@ -60,6 +60,10 @@ enum {
 #define FENCE_QK8_0 32
 #define FENCE_Q8_0_BLOCK_BYTES 34
 
+/* Arrival counters of fence_gqa_attention_qk_f16_arrive: uint32 words per
+ * query head (each counter has a 256-byte slot of its own). */
+#define FENCE_ARRIVE_WORDS_PER_HEAD 64
+
 /* ---------------------------------------------------------------------------
  * One-to-one replacements of the reference launchers (same argument order and
  * meaning; the stream argument is required in the C ABI).
@@ -266,6 +270,22 @@ int fence_gqa_attention_qk_f16(float* attn_out, void* out_f16, float* q, float* 
                                int max_ctx, float eps, float freq_base, int style,
                                float* score_buf, int64_t score_buf_floats,
                                hipStream_t stream);
+
+/* fence_gqa_attention_qk_f16 in one launch where it would take two: no
+ * counterpart in the reference (it replaces the same qwen3.cu:292-310 chain).
+ * The last workgroup to finish the positions of a group of query heads merges
+ * that group's split partials itself, instead of a second kernel merging all
+ * of them.  arrive: n_q_heads * FENCE_ARRIVE_WORDS_PER_HEAD uint32 words that
+ * the caller zeroes once before the first call; every call leaves them zero.  Outputs and cache rows
+ * are bit-identical to fence_gqa_attention_qk_f16's.  Calls that overlap
+ * (other streams) must not share arrive or score_buf. */
+int fence_gqa_attention_qk_f16_arrive(float* attn_out, void* out_f16, float* q, float* k,
+                                      const float* v, const float* q_norm_w,
+                                      const float* k_norm_w, void* k_cache, void* v_cache,
+                                      int head_dim, int n_q_heads, int n_kv_heads, int pos,
+                                      int max_ctx, float eps, float freq_base, int style,
+                                      float* score_buf, int64_t score_buf_floats,
+                                      uint32_t* arrive, hipStream_t stream);
 
 /* out_t = RoPE(rms_norm(x_t, w)) for x [tokens][n_q_heads*head_dim],
  * w [n_q_heads*head_dim], the normalised row viewed as n_q_heads heads; k

@@ -153,6 +153,7 @@ private:
     void* kv_arena_ = nullptr;
     void* scratch_arena_ = nullptr;
     int* host_token_ = nullptr;  // pinned
+    uint32_t* attn_arrive_ = nullptr;  // the one-launch attention's counters, zero between calls
     hipStream_t stream_ = nullptr;
     bool own_stream_ = false;
     Qwen3Sequence sequence_ = Qwen3Sequence::Fused;

@@ -154,6 +154,7 @@ struct Scratch {  // the reference's ScratchBuffers (src/model/qwen3.h:91-112)
     half* x_half;
     half* act_half;  // SwiGLU output of the fused sequence (x_half is its input)
     int* argmax_out;
+    uint32_t* arrive;  // attention's arrival counters (zeroed once; every call leaves them zero)
     void alloc() {
         hidden = dalloc<float>(E), residual = dalloc<float>(E), normed = dalloc<float>(E), q = dalloc<float>(QD),
         k = dalloc<float>(KVD), v = dalloc<float>(KVD), attn_out = dalloc<float>(QD), gate = dalloc<float>(FF),
@@ -162,6 +163,8 @@ struct Scratch {  // the reference's ScratchBuffers (src/model/qwen3.h:91-112)
         x_half = dalloc<half>(FF);
         act_half = dalloc<half>(FF);
         argmax_out = dalloc<int>(1);
+        arrive = dalloc<uint32_t>(NQ * FENCE_ARRIVE_WORDS_PER_HEAD);
+        HIP_CHECK(hipMemset(arrive, 0, NQ * FENCE_ARRIVE_WORDS_PER_HEAD * sizeof(uint32_t)));
     }
 };
 
@@ -209,8 +212,9 @@ void layer_fused(const Layer& L, Scratch& s, int pos, hipStream_t st) {
     const fence_rms_input attn_in{s.hidden, s.tmp, s.residual, L.attn_norm, s.x_half, EPS};
     fence_gemv_q6k_multi_rms(3, w_qkv, y_qkv, nullptr, m_qkv, &attn_in, E, st);
     std::swap(s.hidden, s.residual);
-    fence_gqa_attention_qk_f16(nullptr, s.x_half, s.q, s.k, s.v, L.q_norm, L.k_norm, L.kc, L.vc, HD, NQ, NKV, pos, CTX,
-                               EPS, BASE, FENCE_ROPE_NEOX, s.score_buf, 4 * int64_t(NQ) * CTX, st);
+    fence_gqa_attention_qk_f16_arrive(nullptr, s.x_half, s.q, s.k, s.v, L.q_norm, L.k_norm, L.kc, L.vc, HD, NQ, NKV,
+                                      pos, CTX, EPS, BASE, FENCE_ROPE_NEOX, s.score_buf, 4 * int64_t(NQ) * CTX,
+                                      s.arrive, st);
     fence_gemv_q6k(L.wo, s.x_half, s.tmp, E, QD, st);
     const fence_rms_input ffn_in{s.hidden, s.tmp, s.residual, L.ffn_norm, s.x_half, EPS};
     fence_gemv_q6k_swiglu_rms_f16(L.wg, L.wu, &ffn_in, s.act_half, nullptr, FF, E, st);

@@ -120,6 +120,12 @@ def _raw(name):
     ("fence_gemv_q6k_swiglu_f16", (16, 32, 48, 64, None, -1, 256, None)),
     ("fence_gemv_q6k_swiglu_f16", (16, 32, 48, None, None, 8, 256, None)),  # out_f16 missing
     ("fence_gemv_q6k_swiglu_f16", (16, 0x1001, 48, 64, None, 8, 256, None)),  # W_up misaligned
+    ("fence_gqa_attention_qk_f16_arrive", (None, 16, 32, 48, 64, 80, 96, 112, 128, 128, 8, 2, 5, 100, 1e-6, 1e6,
+                                           0, 144, 0, None, None)),   # no arrival counters
+    ("fence_gqa_attention_qk_f16_arrive", (None, 16, 32, 48, 64, 80, 96, 112, 128, 128, 8, 2, 5, 100, 1e-6, 1e6,
+                                           0, 144, 0, 0x1002, None)),  # counters misaligned
+    ("fence_gqa_attention_qk_f16_arrive", (None, 16, 32, 48, 64, 80, 96, 112, 128, 128, 8, 2, 100, 100, 1e-6, 1e6,
+                                           0, 144, 0, 160, None)),     # pos == max_ctx
     ("fence_gqa_attention", (16, 32, 48, 64, 128, 6, 4, 10, 100, 80, None)),   # 6 % 4 != 0
     ("fence_gqa_attention", (16, 32, 48, 64, 128, 8, 2, 101, 100, 80, None)),  # seq_len > max_ctx
     ("fence_store_kv", (16, 32, 48, 64, 100, 512, 100, None)),                # pos == max_ctx

@@ -110,6 +110,8 @@ def test_decode_step_in_a_graph():
     x16 = torch.empty(E, dtype=torch.int16, device="cuda")
     q, k, v = (torch.empty(n, device="cuda") for n in (QD, KVD, KVD))
     att16 = torch.empty(QD, dtype=torch.int16, device="cuda")
+    att16b = torch.empty(QD, dtype=torch.int16, device="cuda")
+    arrive = torch.zeros(nq * F.ARRIVE_WORDS_PER_HEAD, dtype=torch.int32, device="cuda")
     o, d = torch.empty(E, device="cuda"), torch.empty(E, device="cuda")
     act16 = torch.empty(ff, dtype=torch.int16, device="cuda")
     normed = torch.empty(E, device="cuda")
@@ -117,8 +119,9 @@ def test_decode_step_in_a_graph():
     tok = torch.empty(1, dtype=torch.int32, device="cuda")
     tok_na = torch.empty(1, dtype=torch.int32, device="cuda")
     ws = torch.empty(4 * nq * ctx, device="cuda")
+    ws2 = torch.empty(4 * nq * ctx, device="cuda")
     LIVE.extend([Wq, Wk, Wv, Wo, Wg, Wu, Wd, table, an, fn, qn, kn, on, kc, vc, kc0, vc0, hidden, res, h1, h2, x16,
-                 q, k, v, att16, o, d, act16, normed, logits, tok, tok_na, ws])
+                 q, k, v, att16, att16b, arrive, o, d, act16, normed, logits, tok, tok_na, ws, ws2])
     rin_a = F.rms_input(hidden.data_ptr(), res.data_ptr(), h1.data_ptr(), an.data_ptr(), x16.data_ptr(), 1e-6)
     rin_f = F.rms_input(h1.data_ptr(), o.data_ptr(), h2.data_ptr(), fn.data_ptr(), x16.data_ptr(), 1e-6)
 
@@ -132,6 +135,10 @@ def test_decode_step_in_a_graph():
         F.gqa_attention_qk_f16(None, att16.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), qn.data_ptr(),
                                kn.data_ptr(), kc.data_ptr(), vc.data_ptr(), hd, nq, nkv, pos, ctx, 1e-6, 1e6,
                                F.ROPE_NEOX, ws.data_ptr(), ws.numel(), sh)
+        # the one-launch form (same q, k, v: the launch above leaves them as they were)
+        F.gqa_attention_qk_f16_arrive(None, att16b.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      qn.data_ptr(), kn.data_ptr(), kc.data_ptr(), vc.data_ptr(), hd, nq, nkv, pos,
+                                      ctx, 1e-6, 1e6, F.ROPE_NEOX, ws2.data_ptr(), ws2.numel(), arrive.data_ptr(), sh)
         F.gemv_q6k(Wo.data_ptr(), att16.data_ptr(), o.data_ptr(), E, QD, sh)
         F.gemv_q6k_swiglu_rms_f16(Wg.data_ptr(), Wu.data_ptr(), rin_f, act16.data_ptr(), None, ff, E, sh)
         F.gemv_q6k(Wd.data_ptr(), act16.data_ptr(), d.data_ptr(), E, ff, sh)
@@ -145,5 +152,7 @@ def test_decode_step_in_a_graph():
 
     # every run recomputes h1, h2 (h2 = h1 + o, then += d) and q/k/v from the unchanged inputs;
     # only the caches' row pos carries over, and reset() restores it
-    check_graph(run, [q, k, v, att16, o, act16, d, normed, logits, tok, tok_na, kc, vc, h1, h2], reset)
+    # (arrive is state, not an output: it must be zero at every call, so it is not clobbered)
+    check_graph(run, [q, k, v, att16, att16b, o, act16, d, normed, logits, tok, tok_na, kc, vc, h1, h2], reset)
     assert int(tok_na.item()) == int(tok.item())
+    assert np.array_equal(bits(att16b), bits(att16)) and not bits(arrive).any()
