@@ -52,6 +52,14 @@ def test_model_headers_declare_and_library_exports_everything(fence):
     assert set(fence_model.SIGNATURES) == set(decls)
 
 
+def test_header_constants_match_the_binding():
+    """The #define'd sizes the Python binding restates (fence_ops.py)."""
+    text = open(HEADER).read()
+    defines = dict(re.findall(r"^#define\s+(FENCE_\w+)\s+(\d+)", text, re.M))
+    assert int(defines["FENCE_ARRIVE_WORDS_PER_HEAD"]) == fence_ops.ARRIVE_WORDS_PER_HEAD
+    assert int(defines["FENCE_QK8_0"]) == 32 and int(defines["FENCE_Q8_0_BLOCK_BYTES"]) == 34
+
+
 def test_version_and_status_strings(fence):
     assert "gfx950" in fence.version()
     assert fence.status_string(0) == "success"

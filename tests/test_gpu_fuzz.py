@@ -413,6 +413,32 @@ def test_fuzz_attention_qk_equals_two_calls(seed):
         assert np.array_equal(g.view(kind), r.view(kind)), f"{what}: {part}"
 
 
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_attention_qk_arrive_equals_two_launches(seed):
+    """fence_gqa_attention_qk_f16_arrive (the last workgroup of each head group
+    merges the splits) against fence_gqa_attention_qk_f16 (split + merge
+    kernels): outputs and caches bit for bit, arrival counters zero after."""
+    from test_gpu_attention_arrive import Setup, bits_equal, operands
+    rng = np.random.default_rng(17000 + seed)
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    nq = nkv * int(rng.choice([1, 2, 3, 4, 5, 8]))
+    hd = int(rng.choice([128, 128, 128, 64]))
+    ctx = int(rng.integers(1, 4200))
+    pos = int(rng.choice([0, ctx - 1, int(rng.integers(0, ctx)), min(ctx - 1, 64 * int(rng.integers(0, 40)))]))
+    norm = bool(rng.integers(0, 4))
+    style = int(rng.choice([NEOX, INTERLEAVED]))
+    ws_floats = int(rng.choice([1, 2, 4])) * nq * ctx + int(rng.integers(0, 200))
+    s = Setup(operands(rng, nq, nkv, hd, ctx, norm), ws_floats)
+    what = f"seed {seed}: attention_qk_arrive {nq}/{nkv}x{hd} pos {pos} ctx {ctx} norm {norm} style {style} ws {ws_floats}"
+    ref32, ref16 = s.call(pos, style, arrive=False)
+    kc, vc = s.kcd.clone(), s.vcd.clone()
+    got32, got16 = s.call(pos, style, arrive=True)
+    assert bits_equal(got32, ref32), f"{what}: fp32 out"
+    assert bits_equal(got16, ref16), f"{what}: binary16 out"
+    assert bits_equal(s.kcd, kc) and bits_equal(s.vcd, vc), f"{what}: caches"
+    assert not host(s.arrive).any(), f"{what}: arrival counters left nonzero"
+
+
 # ------------------------------------------- Q6_K launches of several matrices
 
 def q6k_shape(rng, max_blocks=40, budget=6_000_000):
