@@ -127,6 +127,32 @@ def test_arrive_repeated_calls_random_positions():
     assert not bad, f"calls differing from the two-launch form (index, pos, ws_floats, style): {bad[:10]}"
 
 
+def test_arrive_two_streams_at_once():
+    """Two operand sets, each with its own counters and score_buf, called on
+    two streams with nothing ordering one stream's calls against the other's:
+    every output bit-equal to the two-launch form's.  Positions increase, so
+    the cache rows a call attends to were written before it in both passes."""
+    torch = torch_mod()
+    nq, nkv, hd, ctx, n = 32, 8, 128, 4096, 30
+    rng = np.random.default_rng(77)
+    sets = [Setup(operands(rng, nq, nkv, hd, ctx, True), 4 * nq * ctx) for _ in range(2)]
+    pos = [np.sort(rng.choice(ctx, n, replace=False)) for _ in range(2)]
+    ref = {(k, i): sets[k].call(int(pos[k][i]), F.ROPE_NEOX, arrive=False) for i in range(n) for k in range(2)}
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    got = {}
+    for i in range(n):
+        for k in range(2):
+            with torch.cuda.stream(streams[k]):
+                got[(k, i)] = sets[k].call(int(pos[k][i]), F.ROPE_NEOX, arrive=True)
+    torch.cuda.synchronize()
+    bad = [(k, i, int(pos[k][i])) for (k, i) in got
+           if not (torch.equal(got[(k, i)][0].view(torch.int32), ref[(k, i)][0].view(torch.int32))
+                   and torch.equal(got[(k, i)][1], ref[(k, i)][1]))]
+    assert not bad, f"(stream, call, pos) differing from the two-launch form: {bad[:10]}"
+    assert not any(bool(s.arrive.any()) for s in sets), "arrival counters left nonzero"
+
+
 def test_arrive_rejects_missing_counters():
     torch = torch_mod()
     nq, nkv, hd, ctx = 8, 2, 128, 64
