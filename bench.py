@@ -1336,7 +1336,8 @@ def practical_ceiling(torch, F, reps):
 
 
 def copy_calibration(torch):
-    """Device-to-device copy of 1 GiB: the practical streaming ceiling."""
+    """torch's device-to-device copy of 1 GiB, reported beside the stream
+    kernel's ceiling (it is not one: the library's streams beat it)."""
     n = (1 << 30) // 4
     src = torch.empty(n, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
