@@ -22,6 +22,7 @@
 #include "head_math.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 // Workgroups the split-K grid aims for (splits are also capped by score_buf).
 #ifndef FENCE_ATTN_GT_MAX
@@ -45,6 +46,18 @@
 #endif
 static_assert(FENCE_ATTN_ARRIVE_STRIDE >= 1 && FENCE_ATTN_ARRIVE_STRIDE <= FENCE_ARRIVE_WORDS_PER_HEAD,
               "arrival counter stride");
+// Sub-chunks of K and V rows a split workgroup holds in flight: 2 loads the
+// next sub-chunk's rows while the current one is computed (and the first two
+// before the prologue); 1 (kept) loads each sub-chunk after the previous one
+// is done.  The arithmetic, and so every result, is the same either way.
+// Measured on MI355X, Qwen3-4B decode steps (bench.py --decode-only, 64
+// tokens, interleaved runs against a `make TAG=kv2
+// EXTRA=-DFENCE_ATTN_KV_BUFS=2` build): 1,706-1,707 us per token with 1
+// against 1,717-1,721 with 2, whose split kernel needs 161 VGPRs (92).
+#ifndef FENCE_ATTN_KV_BUFS
+#define FENCE_ATTN_KV_BUFS 1
+#endif
+static_assert(FENCE_ATTN_KV_BUFS == 1 || FENCE_ATTN_KV_BUFS == 2, "K/V buffers: 1 or 2");
 
 namespace fence {
 namespace {
@@ -124,8 +137,9 @@ __device__ __forceinline__ float merge_splits_small(Load ld, int splits, int d, 
 // so q is bit-identical to theirs; the workgroups whose range holds position
 // pos also prepare that position's k and v in LDS and attend to it from
 // there (the cache row is never read), and the first head group's one writes
-// the row to the caches.  The first sub-chunk's K and V loads are issued
-// before the prologue, which runs while they are in flight.
+// the row to the caches.  The first sub-chunk's K and V loads (the first
+// two sub-chunks' with FENCE_ATTN_KV_BUFS 2) are issued before the
+// prologue, which runs while they are in flight.
 // ARRIVE (with !FINAL, at most kWave splits): no merge launch.  The partials
 // are written with device-coherent stores (agent-scope atomic stores, which
 // write through the XCD's L2); once they have completed, the workgroup bumps
@@ -216,11 +230,18 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
 
     const uint16_t* kbase = kc + static_cast<int64_t>(kvh) * HD + 8 * sl;
     const uint16_t* vbase = vc + static_cast<int64_t>(kvh) * HD + 8 * sl;
-    h8 kr[kPPG], vr[kPPG];
-    bool on[kPPG];
-    // The sub-chunk's K and V rows, all loads first.  Clamped: a valid cached
-    // position; with ROPE never row pos, which this launch is writing.
-    auto load_kv = [&](int t0) {
+    constexpr int NB = FENCE_ATTN_KV_BUFS;
+    h8 kbuf[NB][kPPG], vbuf[NB][kPPG];
+    bool onbuf[NB][kPPG];
+    using Slot0 = std::integral_constant<int, 0>;
+    using Slot1 = std::integral_constant<int, NB - 1>;
+    // The sub-chunk's K and V rows into buffer `slot`, all loads first.
+    // Clamped: a valid cached position; with ROPE never row pos, which this
+    // launch is writing.
+    auto load_kv = [&](int t0, auto slot) {
+        h8(&kr)[kPPG] = kbuf[decltype(slot)::value];
+        h8(&vr)[kPPG] = vbuf[decltype(slot)::value];
+        bool(&on)[kPPG] = onbuf[decltype(slot)::value];
 #pragma unroll
         for (int i = 0; i < kPPG; ++i) {
             const int t = t0 + pg + kPG * i;
@@ -231,7 +252,10 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
             vr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(vbase + tc * kv_dim));
         }
     };
-    auto process = [&](int t0) {
+    auto process = [&](int t0, auto slot) {
+        h8(&kr)[kPPG] = kbuf[decltype(slot)::value];
+        h8(&vr)[kPPG] = vbuf[decltype(slot)::value];
+        const bool(&on)[kPPG] = onbuf[decltype(slot)::value];
         if constexpr (QK) {
             if (has_pos) {  // position pos from the prologue's rows
 #pragma unroll
@@ -307,7 +331,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         ++sub;
     };
 
-    if (t_begin < t_end) load_kv(t_begin);
+    if (t_begin < t_end) load_kv(t_begin, Slot0{});
+    if (NB == 2 && t_begin + kSub < t_end) load_kv(t_begin + kSub, Slot1{});
     if constexpr (QK) {
         // Unit u < kUnits: q head g = u / G (u < G * GT), else the k head;
         // elements [4i, 4i + 4) and [HALF + 4i, HALF + 4i + 4), i = u % G.
@@ -367,10 +392,23 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
             qv[g][4] = b.x, qv[g][5] = b.y, qv[g][6] = b.z, qv[g][7] = b.w;
         }
     }
-    if (t_begin < t_end) process(t_begin);
-    for (int t0 = t_begin + kSub; t0 < t_end; t0 += kSub) {
-        load_kv(t0);
-        process(t0);
+    if constexpr (NB == 1) {
+        if (t_begin < t_end) process(t_begin, Slot0{});
+        for (int t0 = t_begin + kSub; t0 < t_end; t0 += kSub) {
+            load_kv(t0, Slot0{});
+            process(t0, Slot0{});
+        }
+    } else {
+        // sub-chunks alternate buffers; each buffer is refilled with the
+        // sub-chunk after next as soon as it has been computed
+        for (int t0 = t_begin; t0 < t_end; t0 += 2 * kSub) {
+            process(t0, Slot0{});
+            if (t0 + 2 * kSub < t_end) load_kv(t0 + 2 * kSub, Slot0{});
+            if (t0 + kSub < t_end) {
+                process(t0 + kSub, Slot1{});
+                if (t0 + 3 * kSub < t_end) load_kv(t0 + 3 * kSub, Slot1{});
+            }
+        }
     }
 
     // Sum the position groups' outputs (they share the running maximum).

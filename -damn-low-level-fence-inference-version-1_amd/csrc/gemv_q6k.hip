@@ -77,6 +77,47 @@
 #define FENCE_GEMV_Q6K_XW_ROWS 8192
 #endif
 
+// Gate/up pairs of rows of at most 16 blocks: 0 the staged pair kernel (a
+// row's gate and up on different waves); 4 or 8 the kernel with one wave per
+// output row (gemv_q6k_pairw_kernel), that many waves per workgroup.  Results
+// are the same bits either way.  Measured on MI355X, Qwen3-4B decode steps
+// (bench.py --decode-only, 64 tokens, two interleaved runs of each build):
+// 0: 1,710-1,713 us per token; 8 with the prefetch (kept): 1,683-1,684, and
+// 1,691-1,694 without it; 4: 1,688-1,691, and 1,704-1,707 without it.
+#ifndef FENCE_GEMV_Q6K_PAIRW
+#define FENCE_GEMV_Q6K_PAIRW 8
+#endif
+static_assert(FENCE_GEMV_Q6K_PAIRW == 0 || FENCE_GEMV_Q6K_PAIRW == 4 || FENCE_GEMV_Q6K_PAIRW == 5 ||
+                  FENCE_GEMV_Q6K_PAIRW == 8 || FENCE_GEMV_Q6K_PAIRW == 10,
+              "FENCE_GEMV_Q6K_PAIRW: 0, 4, 5, 8 or 10");
+// Waves per SIMD the one-wave pair kernel's registers are fitted to: 4 (104
+// VGPRs) or 5 (93, no spills).  More resident waves run slower: decode steps
+// (as above) 1,682 us per token at 4 against 1,685-1,687 at 5 with 8-wave
+// workgroups (two per CU either way), 1,719-1,721 with 4-wave workgroups (20
+// waves per CU), 1,762-1,764 with 5-wave and 1,806-1,808 with 10-wave ones.
+#ifndef FENCE_GEMV_Q6K_PAIRW_WPE
+#define FENCE_GEMV_Q6K_PAIRW_WPE 4
+#endif
+// 1: the one-wave pair kernel loads the next output row while the current
+// one is computed; 0: each row after the previous one.
+#ifndef FENCE_GEMV_Q6K_PAIRW_PF
+#define FENCE_GEMV_Q6K_PAIRW_PF 1
+#endif
+
+// 1: the staged kernel loads a wave's next row group while the current one is
+// computed (as XW launches do) in the one-wave launches with the RMSNorm
+// prologue (q/k/v) -- PF_NORM -- and in launches of several waves per row
+// (down) -- PF_SPLIT; 0: each group after the previous one.  Same results.
+// Measured as above: 1,693 us per token with PF_NORM against 1,685-1,687
+// without (97 VGPRs: 4 waves per SIMD instead of 5), 1,681-1,682 with
+// PF_SPLIT (within the spread of the session's runs).
+#ifndef FENCE_GEMV_Q6K_PF_NORM
+#define FENCE_GEMV_Q6K_PF_NORM 0
+#endif
+#ifndef FENCE_GEMV_Q6K_PF_SPLIT
+#define FENCE_GEMV_Q6K_PF_SPLIT 0
+#endif
+
 // 1: every wave of the staged kernel records its entry and exit times on the
 // device's constant wall clock (100 MHz), its hardware placement and its
 // row-group count into `wave_clock` (read back by fence_wave_clock_read).
@@ -111,14 +152,13 @@ static __device__ __align__(256) uint64_t wave_clock[4 * kWaveClockMax];
 #endif
 }
 
-// groups: the wave's row groups g = blockIdx.x + k * gridDim.x < n_groups
-[[maybe_unused]] __device__ __forceinline__ void wave_clock_leave(int64_t wave, int lane, int64_t n_groups) {
+// groups: the row groups (or rows) the wave computed
+[[maybe_unused]] __device__ __forceinline__ void wave_clock_leave_n(int64_t wave, int lane, int64_t groups) {
 #if FENCE_WAVE_CLOCK
     const uint64_t t = __builtin_amdgcn_s_memrealtime();
     // HW_ID (hardware register 4) and XCC_ID (20), all 32 bits of each
     const uint32_t hw = __builtin_amdgcn_s_getreg(4 | (31 << 11));
     const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (31 << 11));
-    const int64_t groups = n_groups > blockIdx.x ? (n_groups - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
     if (lane == 0 && wave < kWaveClockMax) {
         uint64_t* r = wave_clock + 4 * wave;
         r[1] = t;
@@ -128,8 +168,14 @@ static __device__ __align__(256) uint64_t wave_clock[4 * kWaveClockMax];
 #else
     (void)wave;
     (void)lane;
-    (void)n_groups;
+    (void)groups;
 #endif
+}
+
+// groups: the wave's row groups g = blockIdx.x + k * gridDim.x < n_groups
+[[maybe_unused]] __device__ __forceinline__ void wave_clock_leave(int64_t wave, int lane, int64_t n_groups) {
+    const int64_t groups = n_groups > blockIdx.x ? (n_groups - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    wave_clock_leave_n(wave, lane, groups);
 }
 constexpr int kBlockBytes = 210;
 constexpr int kMaxSegBlocks = 16;  // blocks of one row staged by one wave
@@ -337,7 +383,9 @@ template <int PASSES, int WPR, bool PAIR, bool MULTI, int NORM, bool XW = false,
 __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gemv_q6k_staged_kernel(
     const Q6Job job, const uint16_t* __restrict__ x16, int nb, const RmsIn rin) {
     static_assert(!XW || (PASSES * WPR == 4 && !PAIR && NORM == 0), "XW: four passes, plain rows");
-    constexpr bool PF = XW;  // prefetch the next row group
+    // prefetch the next row group: XW launches, and where the switches below ask
+    constexpr bool PF = XW || (FENCE_GEMV_Q6K_PF_NORM && NORM != 0 && WPR == 1 && !PAIR) ||
+                        (FENCE_GEMV_Q6K_PF_SPLIT && NORM == 0 && WPR > 1 && !PAIR);
     constexpr int NW = staged_waves<WPR, PAIR, NORM>();
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
@@ -624,13 +672,15 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
             __syncthreads();  // red[] is rewritten by the next group
         }
     };
-    if constexpr (PF) {  // the first group's chunks here, every later one's a group ahead
-        int64_t o, lr, a0;
-        int m, nch;
-        uint32_t delta;
-        row_of(blockIdx.x, &o, &m, &lr);
-        seg_of(lr, &a0, &nch, &delta);
-        load_seg(job.W[m], a0, nch, ch);
+    if constexpr (PF) {  // the first group's chunks here (NORM: in the prologue), every later one's a group ahead
+        if constexpr (NORM == 0) {
+            int64_t o, lr, a0;
+            int m, nch;
+            uint32_t delta;
+            row_of(blockIdx.x, &o, &m, &lr);
+            seg_of(lr, &a0, &nch, &delta);
+            load_seg(job.W[m], a0, nch, ch);
+        }
         for (int64_t g = blockIdx.x; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::true_type{});
     } else {
         int64_t g = blockIdx.x;
@@ -642,6 +692,222 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
     }
     if constexpr (CLOCK)
         wave_clock_leave(static_cast<int64_t>(blockIdx.x) * NW + wid, lane, (n_out + kOutPerGroup - 1) / kOutPerGroup);
+}
+
+// Pair kernel with one wave per output row, for rows of at most 16 blocks
+// (q6_wpr == 1: one segment per row).  Wave w of the grid computes output
+// rows o = w, w + W, w + 2W, .. (W waves in the grid): gate row o, then up
+// row o, each staged through an LDS buffer of the wave's own and summed
+// exactly as the staged kernel's one-wave rows are (passes in order, masked
+// block slots adding +0, then the wave sum), and act = silu(g) * u in lane 0
+// -- the staged pair kernel's values, bit for bit.  Gate and up meet in
+// registers, so after the NORM prologue no wave waits for another; the staged
+// pair layout puts a row's gate and up on different waves that meet in LDS
+// behind two barriers per row group.  PF: the next output row's chunks are
+// loaded as soon as the current row's are in LDS and stay in flight while it
+// is computed.  NORM / VW: the staged kernel's prologue (RmsIn), for NW waves.
+// CLOCK: the instrumented copy (FENCE_WAVE_CLOCK builds), whose row-group
+// count is the wave's rows.
+template <int PASSES, int NW, int NORM, int VW, bool PF, bool CLOCK = false>
+__global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENCE_GEMV_Q6K_PAIRW_WPE))) void gemv_q6k_pairw_kernel(const Q6Job job, const uint16_t* __restrict__ x16,
+                                                                  int nb, const RmsIn rin) {
+    constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
+    constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
+    constexpr int kChunkSlots = (kSegBytes / 16 + kWave - 1) / kWave;
+    constexpr uint32_t kPassBytes = 4 * kBlockBytes;
+    constexpr int kStageBytes = NW * 2 * kBufBytes;
+    constexpr int kNormXBytes = 2 * 1024 * PASSES;
+    constexpr int kLdsBytes = NORM && kNormXBytes > kStageBytes ? kNormXBytes : kStageBytes;
+    __shared__ __align__(16) uint8_t lds[kLdsBytes];
+    __shared__ float nred[NORM ? 16 : 1];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    uint8_t* bufg = lds + wid * (2 * kBufBytes);
+    uint8_t* bufu = bufg + kBufBytes;
+    const int bslot = lane >> 4, h = (lane >> 3) & 1, j = lane & 7;
+    const int b0 = 0, b1 = nb;
+    const int64_t row_bytes = static_cast<int64_t>(nb) * kBlockBytes;
+    const int64_t n_out = job.end[0];
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * NW;
+    const int64_t o0 = static_cast<int64_t>(blockIdx.x) * NW + wid;
+    if constexpr (CLOCK) wave_clock_enter(o0, lane);
+
+    uint32_t xh[PASSES][8];
+    float kb[PASSES][4];
+    if constexpr (!NORM) load_x<PASSES>(xh, kb, x16, b0, b1, bslot, h, j);
+
+    static_assert(NORM == 0 || (VW >= 1 && VW * NW <= 16 + NW - 1), "VW: 1 .. ceil(16 / NW) slots");
+    constexpr int kVW = NORM ? VW : 1;
+    constexpr int kVpt = NORM ? NORM : 1;
+    f4 nh[kVW][kVpt], nr[kVW][kVpt], nw[kVW][kVpt];
+    auto norm_slot = [&](int i, int jj, int* f) {
+        const int vw = wid + NW * i;
+        *f = vw * kWave + lane + jj * rin.T;
+        return vw * kWave < rin.T && *f < nb * 64;
+    };
+    if constexpr (NORM != 0) {
+        const float* rp = rin.res ? rin.res : rin.hid;
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) {
+                int f;
+                const int fc = norm_slot(i, jj, &f) ? f : 0;
+                nh[i][jj] = ld4<false>(rin.hid + 4 * fc);
+                nr[i][jj] = ld4<false>(rp + 4 * fc);
+                nw[i][jj] = ld4<false>(rin.w + 4 * fc);
+            }
+        }
+    }
+    bool on[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) on[p] = b0 + 4 * p + bslot < b1;
+    const uint32_t lane_ql = 64 * h + 4 * j;
+    const uint32_t lane_qh = 128 + 32 * h + 4 * j;
+    const uint32_t lane_sc = 192 + 8 * h + (j >> 2);
+    const uint32_t blk_off = static_cast<uint32_t>(bslot) * kBlockBytes;
+
+    // The 16-byte chunks covering row lr (the same for gate and up, which
+    // share the shape): [a0, a0 + 16 * nch) of either matrix.
+    auto seg_of = [&](int64_t lr, int64_t* a0, int* nch, uint32_t* delta) {
+        const int64_t start = lr * row_bytes;
+        const int64_t end = start + row_bytes;
+        *a0 = start & ~int64_t(15);
+        *nch = static_cast<int>((end - *a0 + 15) >> 4);
+        *delta = static_cast<uint32_t>(start - *a0);
+    };
+    auto load_seg = [&](const uint8_t* Wm, int64_t a0, int nch, u4* ch) {
+        const uint8_t* src = Wm + a0;
+#pragma unroll
+        for (int k = 0; k < kChunkSlots; ++k) {
+            const int cc = lane + kWave * k;
+            uint32_t off = 16u * static_cast<uint32_t>(cc < nch ? cc : 0);
+            asm volatile("" : "+v"(off));
+            ch[k] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(src + off));
+        }
+    };
+    auto stage = [&](uint8_t* buf, int nch, const u4* ch) {
+#pragma unroll
+        for (int k = 0; k < kChunkSlots; ++k) {
+            const int cc = lane + kWave * k;
+            // a lane past the row's last chunk stores into the slack at the
+            // buffer's end, which holds no block data
+            const uint32_t dst = cc < nch ? 16u * cc : static_cast<uint32_t>(kBufBytes - 16);
+            *reinterpret_cast<u4*>(buf + dst) = ch[k];
+        }
+    };
+    // The lane's sum over the row staged in buf, in the staged kernel's order.
+    auto row_part = [&](const uint8_t* buf, uint32_t delta) {
+        const uint32_t base = delta + blk_off;
+        const uint32_t sh = base & 3u;
+        const uint8_t* ab = buf + (base & ~3u);
+        const uint8_t* bb = buf + base;
+        float part = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const uint32_t* wa = reinterpret_cast<const uint32_t*>(ab + p * kPassBytes + lane_ql);
+            const uint32_t* wb = reinterpret_cast<const uint32_t*>(ab + p * kPassBytes + lane_ql + 32);
+            const uint32_t* wc = reinterpret_cast<const uint32_t*>(ab + p * kPassBytes + lane_qh);
+            const uint32_t a = __builtin_amdgcn_alignbyte(wa[1], wa[0], sh);
+            const uint32_t bq = __builtin_amdgcn_alignbyte(wb[1], wb[0], sh);
+            const uint32_t c = __builtin_amdgcn_alignbyte(wc[1], wc[0], sh);
+            const int8_t* scb = reinterpret_cast<const int8_t*>(bb + p * kPassBytes + lane_sc);
+            int sc[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sc[q] = scb[2 * q];
+            const uint16_t dbits = *reinterpret_cast<const uint16_t*>(bb + p * kPassBytes + 208);
+            const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+            const float v = q6_lane_dot(q6_unpack(a, bq, c), xh[p], kb[p], sc, d);
+            part += on[p] ? v : 0.0f;
+        }
+        return part;
+    };
+
+    u4 chg[kChunkSlots], chu[kChunkSlots];
+    auto load_row = [&](int64_t o) {
+        int64_t a0;
+        int nch;
+        uint32_t delta;
+        seg_of(o < n_out ? o : n_out - 1, &a0, &nch, &delta);
+        load_seg(job.W[0], a0, nch, chg);
+        load_seg(job.W[1], a0, nch, chu);
+    };
+    // The first row's chunks go out before anything else waits.
+    if (o0 < n_out) load_row(o0);
+    if constexpr (NORM != 0) {
+        const int nvw = rin.T / kWave;
+        const bool has_res = rin.res != nullptr;
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) {
+                int f;
+                const bool ok = norm_slot(i, jj, &f);
+                const f4 hv = has_res ? nh[i][jj] + nr[i][jj] : nh[i][jj];
+                nh[i][jj] = ok ? hv : f4(0.0f);
+                if (blockIdx.x == 0 && has_res && ok) st4<false>(rin.hid_out + 4 * f, hv);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+            const int vw = wid + NW * i;
+            if (vw < nvw) {
+                float ss = 0.0f;
+                ss += dot4(nh[i][0]);
+                ss += kVpt > 1 ? dot4(nh[i][kVpt - 1]) : 0.0f;
+                ss = wave_reduce(ss, OpAdd{});
+                if (lane == 0) nred[vw] = ss;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVW; ++i)
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) nw[i][jj] = nw[i][jj] * nh[i][jj];
+        __syncthreads();
+        float tot = nred[0];
+        for (int v = 1; v < nvw; ++v) tot += nred[v];
+        const float rs = rsqrtf(tot / static_cast<float>(nb * 256) + rin.eps);
+        uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+#pragma unroll
+            for (int jj = 0; jj < kVpt; ++jj) {
+                int f;
+                if (norm_slot(i, jj, &f)) {
+                    const f4 o = nw[i][jj] * rs;  // (w * h) * rs
+                    st_h4<false>(xs + 4 * f, o);
+                    if (blockIdx.x == 0) st_h4<false>(rin.x_out + 4 * f, o);
+                }
+            }
+        }
+        __syncthreads();
+        load_x<PASSES>(xh, kb, xs, b0, b1, bslot, h, j);
+        __syncthreads();  // lds holds staged rows from here on
+    }
+    for (int64_t o = o0; o < n_out; o += waves) {  // wave-uniform
+        int64_t a0;
+        int nch;
+        uint32_t delta;
+        seg_of(o, &a0, &nch, &delta);
+        if (!PF && o != o0) load_row(o);
+        __builtin_amdgcn_sched_barrier(0);
+        stage(bufg, nch, chg);
+        stage(bufu, nch, chu);
+        if constexpr (PF) {
+            if (o + waves < n_out) {
+                load_row(o + waves);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        const float gs = wave_sum(row_part(bufg, delta));
+        const float us = wave_sum(row_part(bufu, delta));
+        if (lane == 0) {
+            const float act = silu_mul(gs, us);
+            job.act16[o] = f32_to_f16_bits(act);
+            if (job.act32) job.act32[o] = act;
+        }
+    }
+    if constexpr (CLOCK) wave_clock_leave_n(o0, lane, o0 < n_out ? (n_out - o0 + waves - 1) / waves : 0);
 }
 
 // The lane's value of block b of row lr (its 16 weights), for the direct
@@ -789,6 +1055,51 @@ int launch_staged(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, co
     }
 }
 
+// The one-wave pair kernel (FENCE_GEMV_Q6K_PAIRW waves per workgroup) for
+// rows of nb <= 16 blocks, on a resident grid.
+template <int PASSES, int NORM, int VW>
+int launch_pairw_vw(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
+    constexpr int nw = FENCE_GEMV_Q6K_PAIRW > 0 ? FENCE_GEMV_Q6K_PAIRW : 4;
+    static std::atomic<int> cache[64];
+    constexpr bool pf = FENCE_GEMV_Q6K_PAIRW_PF != 0;
+    return launch_grid_as(gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, false>,
+                          gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, FENCE_WAVE_CLOCK != 0>, kWave * nw, cache,
+                          (n_out + nw - 1) / nw, s, job, x, nb, rin);
+}
+
+template <int PASSES, int NORM>
+int launch_pairw_p(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
+    if constexpr (NORM == 0) {
+        return launch_pairw_vw<PASSES, 0, 0>(job, n_out, x, nb, rin, s);
+    } else {
+        constexpr int nw = FENCE_GEMV_Q6K_PAIRW > 0 ? FENCE_GEMV_Q6K_PAIRW : 4;
+        const int vw = (rin.T / kWave + nw - 1) / nw;  // rin.T <= 1024: at most 16 / nw
+        if (vw <= 1) return launch_pairw_vw<PASSES, NORM, 1>(job, n_out, x, nb, rin, s);
+        if (vw == 2) return launch_pairw_vw<PASSES, NORM, 2>(job, n_out, x, nb, rin, s);
+        if constexpr (3 * nw <= 16 + nw - 1) {
+            if (vw == 3) return launch_pairw_vw<PASSES, NORM, 3>(job, n_out, x, nb, rin, s);
+        }
+        if constexpr (4 * nw <= 16 + nw - 1) {
+            if (vw == 4) return launch_pairw_vw<PASSES, NORM, 4>(job, n_out, x, nb, rin, s);
+        }
+        return FENCE_ERROR_INVALID_VALUE;  // not reached: vw <= ceil(16 / nw)
+    }
+}
+
+template <int NORM>
+int launch_pairw(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, const RmsIn& rin, hipStream_t s) {
+    switch (q6_passes(nb)) {  // nb <= 16: one segment of 1-4 passes
+        case 1: return launch_pairw_p<1, NORM>(job, n_out, x, nb, rin, s);
+        case 2: return launch_pairw_p<2, NORM>(job, n_out, x, nb, rin, s);
+        case 3: return launch_pairw_p<3, NORM>(job, n_out, x, nb, rin, s);
+        case 4: return launch_pairw_p<4, NORM>(job, n_out, x, nb, rin, s);
+        default: return FENCE_ERROR_INVALID_VALUE;  // not reached for nb <= 16
+    }
+}
+
+// Whether a pair of rows of nb blocks takes the one-wave pair kernel.
+constexpr bool use_pairw(int nb) { return FENCE_GEMV_Q6K_PAIRW != 0 && nb <= 16 && q6_wpr(nb) == 1; }
+
 // The staged kernel for a row of nb blocks, at q6_wpr / q6_passes.  Only the
 // (PASSES, WPR) pairs the compiled split table produces are instantiated; NORM
 // launches take rows of up to 32 blocks.
@@ -856,17 +1167,21 @@ int gemv_q6k_run(Q6Job& job, const void* xv, int K, bool pair, hipStream_t s, co
         if (staged && nb <= 32 && vec_norm && rms_row_plan(1, K, &T, &r.vpt) && T <= 1024 &&
             (r.vpt == 1 || (r.vpt == 2 && !pair))) {
             r.T = static_cast<int>(T);
-            if (r.vpt == 1)
+            if (r.vpt == 1) {
+                if (pair && use_pairw(nb)) return launch_pairw<1>(job, n_out, nullptr, nb, r, s);
                 return pair ? launch_nb<true, false, 1>(job, n_out, nullptr, nb, r, s)
                             : launch_nb<false, true, 1>(job, n_out, nullptr, nb, r, s);
+            }
             return launch_nb<false, true, 2>(job, n_out, nullptr, nb, r, s);
         }
         if (int st = residual_rms_f16_launch(r.hid_out, r.x_out, r.hid, r.res, r.w, K, r.eps, s)) return st;
         xv = r.x_out;
     }
     const uint16_t* x = static_cast<const uint16_t*>(xv);
-    if (pair)
+    if (pair) {
+        if (staged && use_pairw(nb)) return launch_pairw<0>(job, n_out, x, nb, none, s);
         return staged ? launch_nb<true, false, 0>(job, n_out, x, nb, none, s) : launch_direct<true>(job, n_out, x, nb, s);
+    }
     if (!staged) return launch_direct<false>(job, n_out, x, nb, s);
     // Few rows of 13-16 blocks: one wave per row leaves most SIMDs idle, so
     // the one-wave layout runs spread over four waves per row (bit-identical).
