@@ -7,6 +7,8 @@
 //   b != null: out[i] = a[i] + b[i]   (2 reads, 1 write: SwiGLU's traffic)
 //   b == null: out[i] = a[i]          (1 read, 1 write; out == a is the
 //                                      in-place form, RoPE's traffic)
+//   a == null: out[i] = 0             (1 write: the masked half of the
+//                                      causal softmax's output)
 //
 // Each lane moves VPT float4s of every stream with non-temporal 128-bit loads
 // and stores (the elementwise kernels' memory access), THREADS lanes per
@@ -17,7 +19,8 @@
 namespace fence {
 namespace {
 
-template <int THREADS, int VPT, bool TWO>
+// READS: streams read (0: out = 0, 1: out = a, 2: out = a + b).
+template <int THREADS, int VPT, int READS>
 __global__ __launch_bounds__(THREADS) void calib_stream_kernel(float* out, const float* a, const float* b,
                                                                int64_t n4) {
     const int64_t base = static_cast<int64_t>(blockIdx.x) * (THREADS * VPT) + threadIdx.x;
@@ -25,9 +28,10 @@ __global__ __launch_bounds__(THREADS) void calib_stream_kernel(float* out, const
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t i = base + static_cast<int64_t>(j) * THREADS;
-        if (i < n4) {
+        v[j] = f4(0.0f);
+        if (READS > 0 && i < n4) {
             v[j] = ld4<true>(a + 4 * i);
-            if constexpr (TWO) v[j] += ld4<true>(b + 4 * i);
+            if constexpr (READS == 2) v[j] += ld4<true>(b + 4 * i);
         }
     }
 #pragma unroll
@@ -40,8 +44,9 @@ __global__ __launch_bounds__(THREADS) void calib_stream_kernel(float* out, const
 template <int THREADS, int VPT>
 int calib_launch(float* out, const float* a, const float* b, int64_t n4, hipStream_t s) {
     const unsigned grid = grid_1d(n4, THREADS * VPT);
-    if (b) return launch(calib_stream_kernel<THREADS, VPT, true>, dim3(grid), dim3(THREADS), 0, s, out, a, b, n4);
-    return launch(calib_stream_kernel<THREADS, VPT, false>, dim3(grid), dim3(THREADS), 0, s, out, a, b, n4);
+    if (!a) return launch(calib_stream_kernel<THREADS, VPT, 0>, dim3(grid), dim3(THREADS), 0, s, out, a, b, n4);
+    if (b) return launch(calib_stream_kernel<THREADS, VPT, 2>, dim3(grid), dim3(THREADS), 0, s, out, a, b, n4);
+    return launch(calib_stream_kernel<THREADS, VPT, 1>, dim3(grid), dim3(THREADS), 0, s, out, a, b, n4);
 }
 
 template <int THREADS>
@@ -60,8 +65,8 @@ int calib_vpt(int vpt, float* out, const float* a, const float* b, int64_t n4, h
 extern "C" int fence_calib_stream(float* out, const float* a, const float* b, int64_t n, int threads, int vpt,
                                   hipStream_t stream) {
     using namespace fence;
-    if (!out || !a || n < 0 || n % 4 != 0) return FENCE_ERROR_INVALID_VALUE;
-    if (!aligned(out, 16) || !aligned(a, 16) || (b && !aligned(b, 16))) return FENCE_ERROR_INVALID_VALUE;
+    if (!out || (!a && b) || n < 0 || n % 4 != 0) return FENCE_ERROR_INVALID_VALUE;
+    if (!aligned(out, 16) || (a && !aligned(a, 16)) || (b && !aligned(b, 16))) return FENCE_ERROR_INVALID_VALUE;
     const int64_t n4 = n / 4;
     // one launch's grid must stay within a dispatch's 32-bit lane count
     if (n4 > kMaxLaunchLanes) return FENCE_ERROR_INVALID_VALUE;

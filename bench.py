@@ -461,6 +461,13 @@ def main():
                                      "same size, same cold rotation)"
         per_op["swiglu"]["frac_of_ceiling"] = round(per_op["swiglu"]["GBps"] / c2, 4)
         per_op["rope"]["frac_of_ceiling"] = round(per_op["rope"]["GBps"] / c1, 4)
+        if "stream_causal_softmax_mix" in ceiling:
+            cs = ceiling["stream_causal_softmax_mix"]["GBps"]
+            per_op["softmax"]["frac_of_ceiling"] = round(per_op["softmax"]["GBps"] / cs, 4)
+            # the whole step at its ops' stream ceilings: the attainable rate `value` reads against
+            t_ceil = sum(BYTES[op] / (rate * 1e9) for op, rate in (("softmax", cs), ("swiglu", c2), ("rope", c1)))
+            ceiling["step_GBps"] = round(STEP_BYTES / t_ceil / 1e9, 1)
+            ceiling["step_source"] = "step bytes over the sum of each op's bytes at its mix's stream rate"
 
     cpu = None if args.no_cpu else section("cpu_baseline", lambda: cpu_baseline(args.cpu_seconds))
     cpu_all = None if args.no_cpu else section("cpu_baseline_all_cores",
@@ -492,6 +499,7 @@ def main():
                    "cache": "warm" if args.warm else f"cold ({nsets} rotating buffer sets)",
                    "step_bytes": STEP_BYTES},
         "frac_peak": round(value / PEAK_HBM_GBPS, 4),
+        "frac_of_step_ceiling": round(value / ceiling["step_GBps"], 4) if "step_GBps" in ceiling else None,
         "ops": per_op,
         "roofline": roofline,
         "configs": configs,
@@ -1253,14 +1261,17 @@ CALIB_SHAPES = ((64, 1), (64, 2), (64, 4), (256, 1), (256, 2), (256, 4))  # (lan
 
 
 def practical_ceiling(torch, F, reps):
-    """The attainable streaming rate on this device for the step's two traffic
-    mixes, each under a cold rotation (buffer sets of more than 1 GiB in
-    total, as the headline):
+    """The attainable streaming rate on this device for the step's three
+    traffic mixes, each under a cold rotation (buffer sets of more than 1 GiB
+    in total, as the headline):
       2 reads + 1 write at SwiGLU's size, [8192 x 14336] a + b -> out;
-      1 read + 1 write in place at RoPE's size, Q + K [8192 x 40 x 128].
+      1 read + 1 write in place at RoPE's size, Q + K [8192 x 40 x 128];
+      the causal softmax's bytes: 1 read + 1 write in place over its unmasked
+      scores (32 x 2048 x 2049 / 2) and 1 write of zeros over the masked ones,
+      two launches timed as one (start of the first to end of the second).
     For each: the library's plain float4 stream (fence_calib_stream) at six
     launch shapes, the fastest kept, timed like the ops (kernel start/end
-    events of each launch); and torch's own elementwise kernel on the same
+    events); and for the first two torch's own elementwise kernel on the same
     tensors (torch.mul(a, b, out=o); x.mul_(c)), timed by stream events around
     each launch (which add ~1-2 us of dispatch to a ~200 us launch)."""
     hev = HipEvents()
@@ -1272,12 +1283,12 @@ def practical_ceiling(torch, F, reps):
         r.update(extra)
         return r
 
-    def ours(sets, run, nbytes):
+    def ours(sets, run, nbytes, launches=1):
         for b in sets:
             run(b)
         evs = [(hev.create(), hev.create()) for _ in range(reps)]
         for i in range(reps):
-            F.time_next_launch(*evs[i])
+            F.time_next_launches(*evs[i], launches)
             run(sets[i % len(sets)])
         torch.cuda.synchronize()
         ts = [hev.elapsed_ms(a, b) * 1e3 for a, b in evs]
@@ -1331,6 +1342,33 @@ def practical_ceiling(torch, F, reps):
               f"({100 * tr['frac_peak']:.1f}%)", file=sys.stderr, flush=True)
         del sets
         torch.cuda.empty_cache()
+
+    # the causal softmax's mix: scores in place, then the masked zeros
+    n_rw, n_w = SM_VALID, SM_HEADS * SM_Q * SM_K - SM_VALID
+    nbytes = BYTES["softmax"]
+    nsets = max(2, -(-(1 << 30) // (4 * (n_rw + n_w))) + 1)
+    sets = [torch.randn(n_rw + n_w, device="cuda", generator=gen) for _ in range(nsets)]
+
+    def run_mix(t, v, x):
+        F.calib_stream(x.data_ptr(), x.data_ptr(), None, n_rw, t, v, sh)
+        F.calib_stream(x[n_rw:].data_ptr(), None, None, n_w, t, v, sh)
+    shapes = {}
+    best = None
+    for t, v in CALIB_SHAPES:
+        r = summary(ours(sets, lambda x, t=t, v=v: run_mix(t, v, x), nbytes, launches=2), nbytes,
+                    kernel="calib_stream_kernel", threads=t, float4_per_lane=v)
+        shapes[f"{t}x{v}"] = r["GBps"]
+        if best is None or r["us_mean"] < best["us_mean"]:
+            best = r
+    best["GBps_by_shape"] = shapes
+    best["sets"] = nsets
+    best["read_bytes"], best["write_bytes"] = 4 * n_rw, 4 * (n_rw + n_w)
+    best["timing"] = "kernel start/end events of the two launches (hipExtLaunchKernel)"
+    out["stream_causal_softmax_mix"] = best
+    print(f"[ceiling] causal softmax mix: stream {best['GBps']:.1f} GB/s ({100 * best['frac_peak']:.1f}%, "
+          f"{best['threads']}x{best['float4_per_lane']})", file=sys.stderr, flush=True)
+    del sets
+    torch.cuda.empty_cache()
     out["torch_copy_1GiB_GBps"] = copy_calibration(torch)
     return out
 

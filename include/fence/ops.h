@@ -410,12 +410,13 @@ int fence_time_next_launch(hipEvent_t start, hipEvent_t stop);
  * the last one's end.  count < 1 is FENCE_ERROR_INVALID_VALUE. */
 int fence_time_next_launches(hipEvent_t start, hipEvent_t stop, int count);
 
-/* Calibration stream: out[i] = a[i] + b[i] (b != NULL: 2 reads, 1 write) or
+/* Calibration stream: out[i] = a[i] + b[i] (b != NULL: 2 reads, 1 write),
  * out[i] = a[i] (b == NULL: 1 read, 1 write; out == a is the in-place form)
- * over n floats, with the elementwise kernels' memory access (non-temporal
- * 128-bit loads and stores) at a chosen launch shape: `threads` lanes per
- * workgroup (64 or 256), `vpt` float4s per lane (1, 2 or 4).  n % 4 == 0,
- * every pointer 16-byte aligned and n / 4 <= 2^30, else EINVAL.  No
+ * or out[i] = 0 (a == NULL and b == NULL: 1 write) over n floats, with the
+ * elementwise kernels' memory access (non-temporal 128-bit loads and stores)
+ * at a chosen launch shape: `threads` lanes per workgroup (64 or 256), `vpt`
+ * float4s per lane (1, 2 or 4).  n % 4 == 0, every pointer given 16-byte
+ * aligned, b only with a, and n / 4 <= 2^30, else EINVAL.  No
  * counterpart in the reference; the benchmark times it to report the
  * attainable streaming rate beside each op's. */
 int fence_calib_stream(float* out, const float* a, const float* b, int64_t n, int threads, int vpt,

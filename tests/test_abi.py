@@ -161,6 +161,7 @@ def _raw(name):
     ("fence_calib_stream", (16, 32, 48, 8, 128, 1, None)),         # threads not 64 or 256
     ("fence_calib_stream", (16, 32, None, 8, 64, 3, None)),        # vpt not 1, 2 or 4
     ("fence_calib_stream", (16, 32, None, 8 << 30, 64, 1, None)),  # past one launch
+    ("fence_calib_stream", (16, None, 48, 8, 64, 1, None)),        # b without a
 ])
 def test_invalid_arguments_rejected_on_host(fence, name, args):
     assert _raw(name)(*args) == EINVAL
