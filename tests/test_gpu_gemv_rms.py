@@ -178,6 +178,29 @@ def test_swiglu_rms_equals_norm_then_pair(M, K):
     assert np.array_equal(run_pair(Wg, Wu, M, K, hid, res, w, fp32=False)[0], got16)
 
 
+# The one-wave pair kernel with the norm prologue at its edges: fewer rows
+# than a workgroup's waves, every pass count, no residual; bit for bit the
+# norm launch followed by the pair launch on its binary16 row.
+@pytest.mark.parametrize("nb,M,residual", [
+    (1, 8, True), (3, 8, False), (4, 2, True), (8, 1, True), (9, 8, False), (13, 8, True),
+    (16, 3, True), (10, 4100, False),
+])
+def test_swiglu_rms_one_wave_pair_edges(nb, M, residual):
+    K = 256 * nb
+    rng = np.random.default_rng(7 * M + nb)
+    Wg, Wu = make_q6k_matrix(rng, M, K), make_q6k_matrix(rng, M, K)
+    hid, res, w = row(rng, K, residual)
+    got16, got32, hout, x16 = run_pair(Wg, Wu, M, K, hid, res, w)
+    ref_h, ref_x = unfused_input(hid, res, w, K)
+    assert np.array_equal(x16, ref_x)
+    if residual:
+        assert np.array_equal(hout.view(np.uint32), ref_h.view(np.uint32))
+    import test_gpu_q6k as q6
+    ref16, ref32 = q6.run_swiglu(Wg, Wu, ref_x, M, K)
+    assert np.array_equal(got16, ref16), f"{M} rows of {nb} blocks: binary16 act"
+    assert np.array_equal(got32.view(np.uint32), ref32.view(np.uint32)), f"{M} rows of {nb} blocks: fp32 act"
+
+
 def test_rms_input_rejects_overlap_and_missing_outputs():
     torch = torch_mod()
     K = 512

@@ -337,6 +337,29 @@ def test_gemv_q6k_swiglu_equals_unfused_sequence(oracle, M, K):
     assert np.all(np.abs(got32 - oracle.silu_mul(g, u)) <= bound + 1e-30)
 
 
+# Gate/up pairs of rows of at most 16 blocks take the kernel with one wave per
+# output row (8-wave workgroups, the next row prefetched): every pass count
+# (1-4 passes of four blocks), masked block slots, fewer rows than a
+# workgroup's waves, exactly one workgroup's, and row counts either side of
+# the resident grid's waves, each bit-equal to the two GEMV launches and the
+# SwiGLU launch it replaces.  (M * nb % 8 == 0 keeps them on the staged path.)
+@pytest.mark.parametrize("nb,M", [
+    (1, 8), (1, 64), (2, 4), (3, 8), (4, 2), (5, 8), (8, 1), (8, 7), (8, 9),
+    (9, 8), (12, 6), (13, 8), (16, 1), (16, 3), (16, 8), (10, 4092), (10, 4100), (10, 8196),
+])
+def test_gemv_q6k_swiglu_one_wave_pair_edges(nb, M):
+    K = 256 * nb
+    assert (M * nb) % 8 == 0
+    rng = np.random.default_rng(nb * 1009 + M)
+    Wg, Wu = make_q6k_matrix(rng, M, K), make_q6k_matrix(rng, M, K)
+    x = rand_x(rng, K, std=0.5)
+    got16, got32 = run_swiglu(Wg, Wu, x, M, K)
+    ref16, ref32 = unfused_swiglu(Wg, Wu, x, M, K)
+    what = f"{M} rows of {nb} blocks"
+    assert np.array_equal(got32.view(np.uint32), ref32.view(np.uint32)), what + ": fp32 act"
+    assert np.array_equal(got16, ref16), what + ": binary16 act"
+
+
 def test_gemv_q6k_swiglu_unaligned_weights():
     """W only 2-byte aligned: the direct pair kernel."""
     torch = torch_mod()
