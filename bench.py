@@ -1134,7 +1134,9 @@ def wave_clock(torch, F, reps, raw_path=None):
     prologue, down -- with cold weights (sets rotated over more than 1 GiB)
     and warm inputs, each launch also timed by its kernel start/end events.
     Per launch (medians over `reps`): the span from the first wave's entry to
-    the last wave's exit against the event time; the dispatch ramp (entry
+    the last wave's exit against the event time, and the event time again
+    with the weights already in the caches (`event_warm_us`, the launch after
+    an untimed one on the same weights); the dispatch ramp (entry
     offsets); each wave's lifetime and its time per row group; the tail
     (exit offsets from the last exit); mean resident waves per CU over the
     span against the waves launched per CU."""
@@ -1224,8 +1226,21 @@ def wave_clock(torch, F, reps, raw_path=None):
         med = {key: round(float(np.median([p[key] for p in per])), 3) for key in per[0]}
         med["bytes"] = nbytes
         med["GBps_event"] = round(nbytes / (med["event_us"] * 1e-6) / 1e9, 1)
+        # The same launch with its weights already in the caches (each timed
+        # launch right after an untimed one on the same set): what HBM costs it
+        warm = []
+        for i in range(reps):
+            run(sets[0])
+            e0, e1 = hev.create(), hev.create()
+            F.time_next_launch(e0, e1)
+            run(sets[0])
+            torch.cuda.synchronize()
+            warm.append(hev.elapsed_ms(e0, e1) * 1e3)
+            hev.destroy_all()
+        med["event_warm_us"] = round(float(np.median(warm)), 3)
         out["ops"][name] = med
-        print(f"[wave clock] {name:38s} event {med['event_us']:6.2f} us  span {med['span_us']:6.2f}  "
+        print(f"[wave clock] {name:38s} event {med['event_us']:6.2f} us (warm {med['event_warm_us']:6.2f})  "
+              f"span {med['span_us']:6.2f}  "
               f"waves {int(med['waves'])} on {int(med['cus'])} CUs  ramp p50/p90/max {med['ramp_p50_us']:.2f}/"
               f"{med['ramp_p90_us']:.2f}/{med['ramp_max_us']:.2f}  life {med['life_mean_us']:.2f} "
               f"({int(med['groups_min'])}-{int(med['groups_max'])} groups, {med['us_per_group_mean']:.2f}/group)  "
