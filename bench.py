@@ -464,9 +464,7 @@ def main():
         if "stream_causal_softmax_mix" in ceiling:
             cs = ceiling["stream_causal_softmax_mix"]["GBps"]
             per_op["softmax"]["frac_of_ceiling"] = round(per_op["softmax"]["GBps"] / cs, 4)
-            # the whole step at its ops' stream ceilings: the attainable rate `value` reads against
-            t_ceil = sum(BYTES[op] / (rate * 1e9) for op, rate in (("softmax", cs), ("swiglu", c2), ("rope", c1)))
-            ceiling["step_GBps"] = round(STEP_BYTES / t_ceil / 1e9, 1)
+            ceiling["step_GBps"] = step_ceiling_gbps({"softmax": cs, "swiglu": c2, "rope": c1})
             ceiling["step_source"] = "step bytes over the sum of each op's bytes at its mix's stream rate"
 
     cpu = None if args.no_cpu else section("cpu_baseline", lambda: cpu_baseline(args.cpu_seconds))
@@ -1275,6 +1273,21 @@ def gemv_bytes(m, k):
 CALIB_SHAPES = ((64, 1), (64, 2), (64, 4), (256, 1), (256, 2), (256, 4))  # (lanes per workgroup, float4 per lane)
 
 
+def causal_softmax_mix():
+    """The causal softmax's traffic as two plain streams: (floats read and
+    written in place -- the unmasked scores --, floats only written -- the
+    masked ones).  Their bytes are BYTES["softmax"]."""
+    return SM_VALID, SM_HEADS * SM_Q * SM_K - SM_VALID
+
+
+def step_ceiling_gbps(rates):
+    """The step's attainable rate when each op runs at its traffic mix's
+    plain-stream rate (GB/s per op): step bytes over the sum of the ops'
+    times at those rates."""
+    t = sum(BYTES[op] / (rate * 1e9) for op, rate in rates.items())
+    return round(STEP_BYTES / t / 1e9, 1)
+
+
 def practical_ceiling(torch, F, reps):
     """The attainable streaming rate on this device for the step's three
     traffic mixes, each under a cold rotation (buffer sets of more than 1 GiB
@@ -1359,7 +1372,7 @@ def practical_ceiling(torch, F, reps):
         torch.cuda.empty_cache()
 
     # the causal softmax's mix: scores in place, then the masked zeros
-    n_rw, n_w = SM_VALID, SM_HEADS * SM_Q * SM_K - SM_VALID
+    n_rw, n_w = causal_softmax_mix()
     nbytes = BYTES["softmax"]
     nsets = max(2, -(-(1 << 30) // (4 * (n_rw + n_w))) + 1)
     sets = [torch.randn(n_rw + n_w, device="cuda", generator=gen) for _ in range(nsets)]

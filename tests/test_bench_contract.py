@@ -70,3 +70,19 @@ def test_attainable_is_cold_floor_plus_bytes_at_peak():
     s = res[3]["attainable"]
     assert s["attainable_us"] == 3.5 + 11.0 and s["frac_of_attainable"] == round(14.5 / 14.0, 4)
     assert "attainable" not in res[4] and "attainable" not in res[5]
+
+
+def test_softmax_mix_ceiling_moves_the_softmax_bytes():
+    """The causal softmax's ceiling streams: in place over the unmasked scores
+    (read + write), zeros over the masked ones (write) -- its own bytes."""
+    n_rw, n_w = bench.causal_softmax_mix()
+    assert 8 * n_rw + 4 * n_w == bench.BYTES["softmax"]
+    assert n_rw % 4 == 0 and n_w % 4 == 0  # float4 streams, the second 16-byte aligned
+
+
+def test_step_ceiling_is_the_harmonic_combination():
+    assert bench.step_ceiling_gbps({op: 5000.0 for op in bench.BYTES}) == 5000.0
+    rates = {"softmax": 6400.0, "swiglu": 6800.0, "rope": 6500.0}
+    t = sum(bench.BYTES[op] / (r * 1e9) for op, r in rates.items())
+    assert abs(bench.step_ceiling_gbps(rates) - bench.STEP_BYTES / t / 1e9) < 0.1
+    assert min(rates.values()) < bench.step_ceiling_gbps(rates) < max(rates.values())
