@@ -16,8 +16,9 @@
 // whole group.  16 lanes per position (8 dims each, one 128-bit load of K and
 // one of V per lane); the q . k dot is reduced with DPP inside the 16-lane
 // row.  With one split the workgroup writes the output; otherwise it writes
-// (m, l, o) per head to the caller's score_buf -- the reference's scratch
-// argument -- and a second kernel merges the splits.  Nothing is allocated.
+// o and (m, l) per head to the caller's score_buf -- the reference's
+// scratch argument -- and a second kernel merges the splits.  Nothing is
+// allocated.
 #include "common.hpp"
 #include "head_math.hpp"
 
@@ -92,35 +93,95 @@ struct QkIn {
     InvFreq tab;
 };
 
-// One wave's share of the merge of one query head over splits <= kWave:
-// output dim d, lane = d mod 64.  ld(i) reads float i of the head's partials
-// [splits][HD + 2].  Shared by the merge kernel and the split kernel's
-// last-arrival merge, so both give the same bits.
-template <class Load>
-__device__ __forceinline__ float merge_splits_small(Load ld, int splits, int d, int lane) {
-    constexpr int kRow = 128 + 2;
-    const int sl = lane < splits ? lane : 0;  // clamped: a valid split, dropped below
-    uint32_t ml = static_cast<uint32_t>(sl * kRow);
-    asm volatile("" : "+v"(ml));
-    const float m_l = ld(ml);
-    const float l_l = ld(ml + 1);
-    float os[kWave];
+// Split partials in ws (16-byte aligned), n_q * splits * (128 + 2) floats:
+// the o rows [n_q][splits][128], then the (m, l) pairs [n_q][splits][2].
+constexpr int kHD = 128;
+__device__ __forceinline__ int64_t partial_o_at(int h, int splits, int split) {
+    return (static_cast<int64_t>(h) * splits + split) * kHD;
+}
+__device__ __forceinline__ int64_t partial_ml_at(int n_q, int h, int splits, int split) {
+    return static_cast<int64_t>(n_q) * splits * kHD + (static_cast<int64_t>(h) * splits + split) * 2;
+}
+
+// Buffer resource word 3 for raw dword accesses (DATA_FORMAT 32), and the
+// cache policy (sc1) of an agent-scope atomic load: the arrival merge reads
+// partials that workgroups on other XCDs -- other L2s -- of the same launch
+// wrote.  A buffer access past the resource's size reads 0 and never faults.
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kPolicyDevice = 16;
+
+// One wave's merge of one query head's splits (at most kWave) over dims
+// [64 half, 64 half + 64).  Lane (sg, j) = (lane / 16, lane % 16) loads dims
+// 4j .. 4j + 3 of splits sg, sg + 4, .. (one 128-bit load each, all issued
+// before any use) and lane s the (m, l) of split s.  M = max m_s, c_s =
+// 2^(m_s - M) (0 for an empty split), L = sum l_s c_s by a DPP reduction; each
+// lane adds c_b o_b over its splits in order, the four lane groups are added
+// as (sg0 + sg1) + (sg2 + sg3), and every lane returns the four dims' o / L.
+// Shared by the merge kernel and the split kernel's last-arrival merge, so
+// both give the same bits.
+// A wave-uniform pointer as the compiler's uniform value (lane 0's copy), so
+// a buffer resource built from it needs no per-lane loop.
+__device__ __forceinline__ float* uniform_ptr(const float* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<float*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// o_head and ml_head are wave-uniform.
+template <int POLICY>
+__device__ __forceinline__ f4 merge_head_half(const float* o_head, const float* ml_head, int splits, int half,
+                                              int lane) {
+    const __amdgpu_buffer_rsrc_t ro =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(o_head), 0, splits * kHD * 4, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rml =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(ml_head), 0, splits * 8, kRsrcWord3);
+    const int j = lane & 15, sg = lane >> 4;
+    const f2 ml = __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(rml, lane * 8, 0, POLICY));
+    // Every load is issued and used, with no branch, so the wait counter
+    // stays exact and (m, l)'s arithmetic below overlaps the o loads; splits
+    // past the last read 0 and weigh 0, adding 0 * 0.
+    f4 ov[kWave / 4];
 #pragma unroll
-    for (int b = 0; b < kWave; ++b) {
-        uint32_t ob = static_cast<uint32_t>((b < splits ? b : 0) * kRow + 2 + d);
-        asm volatile("" : "+v"(ob));
-        os[b] = ld(ob);
+    for (int i = 0; i < kWave / 4; ++i) {
+        const int at = ((sg + 4 * i) * kHD + 64 * half + 4 * j) * 4;
+        ov[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(ro, at, 0, POLICY));
     }
-    __builtin_amdgcn_sched_barrier(0);
     const bool on = lane < splits;
-    const float M = wave_reduce(on ? m_l : -__builtin_inff(), OpMax{});
-    const float c_l = (!on || l_l == 0.0f) ? 0.0f : exp2_hw(m_l - M);  // an empty split weighs 0
-    const float L = wave_reduce(on ? l_l * c_l : 0.0f, OpAdd{});
-    float O = 0.0f;
+    const float M = wave_reduce(on ? ml.x : -__builtin_inff(), OpMax{});
+    const float c = (!on || ml.y == 0.0f) ? 0.0f : exp2_hw(ml.x - M);  // an empty split weighs 0
+    const float L = wave_reduce(on ? ml.y * c : 0.0f, OpAdd{});
+    // Lane (sg, j) takes c of split sg + 4j; step i then broadcasts lane
+    // (sg, i)'s copy over the 16-lane row (DPP row_newbcast): c of split
+    // sg + 4i, with no LDS round trip per step.
+    const float ct = __shfl(c, sg + 4 * j, kWave);
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    static_for<0, kWave / 4>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        const float cb = dpp<kDppRowNewBcast0 + i>(ct);
+        acc.x = __builtin_fmaf(cb, ov[i].x, acc.x);
+        acc.y = __builtin_fmaf(cb, ov[i].y, acc.y);
+        acc.z = __builtin_fmaf(cb, ov[i].z, acc.z);
+        acc.w = __builtin_fmaf(cb, ov[i].w, acc.w);
+    });
 #pragma unroll
-    for (int b = 0; b < kWave; ++b)
-        if (b < splits) O = __builtin_fmaf(readlane(c_l, b), os[b], O);
-    return L == 0.0f ? 0.0f : O / L;
+    for (int m = 16; m <= 32; m *= 2) {
+        acc.x += __shfl_xor(acc.x, m, kWave);
+        acc.y += __shfl_xor(acc.y, m, kWave);
+        acc.z += __shfl_xor(acc.z, m, kWave);
+        acc.w += __shfl_xor(acc.w, m, kWave);
+    }
+    if (L == 0.0f) return f4{0.0f, 0.0f, 0.0f, 0.0f};
+    return f4{acc.x / L, acc.y / L, acc.z / L, acc.w / L};
+}
+
+// merge_head_half's outputs: lane (sg, j) writes dim 64 half + 4j + sg.
+__device__ __forceinline__ void write_head_half(float* out, uint16_t* out16, int h, int half, int lane, f4 r) {
+    const int sg = lane >> 4;
+    const float v = sg == 0 ? r.x : sg == 1 ? r.y : sg == 2 ? r.z : r.w;
+    const int64_t at = static_cast<int64_t>(h) * kHD + 64 * half + 4 * (lane & 15) + sg;
+    if (out) out[at] = v;
+    if (out16) out16[at] = f32_to_f16_bits(v);
 }
 
 // Split kernel: grid (n_kv * head_groups, splits); HD = 128.  The workgroup
@@ -236,8 +297,9 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
     using Slot0 = std::integral_constant<int, 0>;
     using Slot1 = std::integral_constant<int, NB - 1>;
     // The sub-chunk's K and V rows into buffer `slot`, all loads first.
-    // Clamped: a valid cached position; with ROPE never row pos, which this
-    // launch is writing.
+    // Clamped: a valid cached position (row 0 for an empty range); with ROPE
+    // never row pos, which this launch is writing, unless pos is 0.
+    const int t_fill = (t_begin < t_end && !(QK && t_begin == pos)) ? t_begin : 0;
     auto load_kv = [&](int t0, auto slot) {
         h8(&kr)[kPPG] = kbuf[decltype(slot)::value];
         h8(&vr)[kPPG] = vbuf[decltype(slot)::value];
@@ -246,8 +308,7 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         for (int i = 0; i < kPPG; ++i) {
             const int t = t0 + pg + kPG * i;
             on[i] = t < t_end;
-            int64_t tc = on[i] ? t : t_begin;
-            if constexpr (QK) tc = (on[i] && t != pos) ? t : (t_begin != pos ? t_begin : 0);
+            const int64_t tc = (on[i] && !(QK && t == pos)) ? t : t_fill;
             kr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(kbase + tc * kv_dim));
             vr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(vbase + tc * kv_dim));
         }
@@ -331,35 +392,50 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         ++sub;
     };
 
-    if (t_begin < t_end) load_kv(t_begin, Slot0{});
-    if (NB == 2 && t_begin + kSub < t_end) load_kv(t_begin + kSub, Slot1{});
+    // Unit u < kUnits: q head g = u / G (u < G * GT), else the k head;
+    // elements [4i, 4i + 4) and [HALF + 4i, HALF + 4i + 4), i = u % G.
+    // Whole waves compute (the DPP rows need every lane); lanes past the
+    // units repeat the k unit and store nothing.  Wave 2 computes the pair
+    // angles' cos and sin meanwhile.  The prologue's loads are issued before
+    // the K and V loads: loads complete in issue order for the wait counter,
+    // so the prologue then runs while the K and V rows are still in flight.
+    const int u = threadIdx.x;
+    const bool unit_wave = QK && wave * kWave < kUnits;  // wave-uniform
+    const bool isk = u >= G * GT;
+    const int iu = u % G;
+    const int gu = isk ? 0 : u / G;
+    f4 a, b, va, vb, wa, wb;
+    float freq = 0.0f;
     if constexpr (QK) {
-        // Unit u < kUnits: q head g = u / G (u < G * GT), else the k head;
-        // elements [4i, 4i + 4) and [HALF + 4i, HALF + 4i + 4), i = u % G.
-        // Whole waves compute (the DPP rows need every lane); lanes past the
-        // units repeat the k unit and store nothing.  Wave 2 computes the
-        // pair angles' cos and sin meanwhile.
-        const int u = threadIdx.x;
-        const bool unit_wave = wave * kWave < kUnits;  // wave-uniform
-        const bool isk = u >= G * GT;
-        const int i = u % G;
-        const int g = isk ? 0 : u / G;
-        f4 a, b, va, vb;
         if (unit_wave) {
             const float* src = isk ? qk.k + static_cast<int64_t>(kvh) * HD
-                                   : q + static_cast<int64_t>(h0 + (g < ng ? g : 0)) * HD;
+                                   : q + static_cast<int64_t>(h0 + (gu < ng ? gu : 0)) * HD;
             const float* vsrc = qk.v + static_cast<int64_t>(kvh) * HD;
-            a = ld4<false>(src + 4 * i);
-            b = ld4<false>(src + HALF + 4 * i);
-            va = ld4<false>(vsrc + 4 * i);
-            vb = ld4<false>(vsrc + HALF + 4 * i);
+            a = ld4<false>(src + 4 * iu);
+            b = ld4<false>(src + HALF + 4 * iu);
+            va = ld4<false>(vsrc + 4 * iu);
+            vb = ld4<false>(vsrc + HALF + 4 * iu);
             if (qk.wq) {  // launch-uniform
                 const float* w = isk ? qk.wk : qk.wq;
-                head_norm_unit<G>(a, b, ld4<false>(w + 4 * i), ld4<false>(w + HALF + 4 * i), qk.eps);
+                wa = ld4<false>(w + 4 * iu);
+                wb = ld4<false>(w + HALF + 4 * iu);
             }
         } else if (wave == 2) {
+            freq = qk.tab.v[lane];
+        }
+    }
+    // Issued whether or not the range is empty (then clamped and unused), so
+    // that every path reaches the prologue's waits with the same loads in
+    // flight and they wait for the prologue's own loads only.
+    load_kv(t_begin, Slot0{});
+    if (NB == 2 && t_begin + kSub < t_end) load_kv(t_begin + kSub, Slot1{});
+    if constexpr (QK) {
+        const int i = iu, g = gu;
+        if (unit_wave) {
+            if (qk.wq) head_norm_unit<G>(a, b, wa, wb, qk.eps);
+        } else if (wave == 2) {
             float sn, cn;
-            sincos_angle(static_cast<float>(pos) * qk.tab.v[lane], &sn, &cn);
+            sincos_angle(static_cast<float>(pos) * freq, &sn, &cn);
             qcs[lane] = cn;
             qcs[HALF + lane] = sn;
         }
@@ -439,20 +515,22 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
             if (out) out[static_cast<int64_t>(h) * HD + d] = r;
             if (out16) out16[static_cast<int64_t>(h) * HD + d] = f32_to_f16_bits(r);
         } else {
-            // partial of (head h, split): [m, l, o[HD]]
-            float* p = ws + (static_cast<int64_t>(h) * gridDim.y + split) * (HD + 2);
+            // partial of (head h, split): o[HD], then (m, l)
+            const int splits = static_cast<int>(gridDim.y);
+            float* po = ws + partial_o_at(h, splits, split);
+            float* pml = ws + partial_ml_at(n_q, h, splits, split);
             if constexpr (ARRIVE) {
                 if (d == 0) {
-                    __hip_atomic_store(p, mg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(p + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(pml, mg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(pml + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
-                __hip_atomic_store(p + 2 + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(po + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 if (d == 0) {
-                    p[0] = mg;
-                    p[1] = l;
+                    pml[0] = mg;
+                    pml[1] = l;
                 }
-                p[2 + d] = acc;
+                po[d] = acc;
             }
         }
     }
@@ -472,66 +550,59 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         if (threadIdx.x == 0)
             __hip_atomic_store(arrive + bx * FENCE_ATTN_ARRIVE_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // The merge of heads h0 .. h0 + ng - 1: wave w takes head-halves
-        // e = w, w + 4, ..: head e / 2, dims 64 (e % 2) + lane.
+        // e = w, w + 4, ..: head e / 2, dims [64 (e % 2), 64 (e % 2) + 64).
         const int splits = static_cast<int>(gridDim.y);
         for (int e = wave; e < 2 * ng; e += kThreads / kWave) {
-            const int h = h0 + e / 2, d = (e % 2) * kWave + lane;
-            const float* p = ws + static_cast<int64_t>(h) * splits * (HD + 2);
-            const float r = merge_splits_small(
-                [p](uint32_t i) { return __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
-                splits, d, lane);
-            if (out) out[static_cast<int64_t>(h) * HD + d] = r;
-            if (out16) out16[static_cast<int64_t>(h) * HD + d] = f32_to_f16_bits(r);
+            const int h = h0 + e / 2;
+            const f4 r = merge_head_half<kPolicyDevice>(ws + partial_o_at(h, splits, 0),
+                                                        ws + partial_ml_at(n_q, h, splits, 0), splits, e % 2, lane);
+            write_head_half(out, out16, h, e % 2, lane, r);
         }
     }
 }
 
-// Merge kernel: one workgroup of HD threads per query head; thread d owns
-// output dim d.  With at most 64 splits everything comes in one round trip:
-// lane s of each wave loads split s's (m_s, l_s), every thread loads its
-// o_s[d] for all splits, all before any use.  Each wave then forms M = max m_s
-// and c_s = 2^(m_s - M) in lane s, L = sum l_s c_s by a DPP reduction (both
-// waves compute the same values), and O = sum_s c_s o_s[d] in split order
-// with c_s read from lane s.  More splits (up to kMaxMergeSplits) take the
-// LDS form: (m, l) through LDS, then the o sums eight loads at a time.
+// Merge kernel: one workgroup of HD threads per query head.  Up to kWave
+// splits, wave w merges dims [64 w, 64 w + 64) with merge_head_half.  More
+// splits (up to kMaxMergeSplits) take the LDS form, thread d owning dim d:
+// (m, l) through LDS, then the o sums eight loads at a time.
 constexpr int kMaxMergeSplits = 1024;
 
 __global__ __launch_bounds__(128) void attn_merge_kernel(float* __restrict__ out, uint16_t* __restrict__ out16,
-                                                         const float* __restrict__ ws, int splits) {
-    constexpr int HD = 128;
-    constexpr int kRow = HD + 2;
+                                                         const float* __restrict__ ws, int n_q, int splits) {
+    constexpr int HD = kHD;
     const int h = blockIdx.x, d = threadIdx.x, lane = threadIdx.x & (kWave - 1);
-    const float* p = ws + static_cast<int64_t>(h) * splits * kRow;
-    float r;
+    const float* po = ws + partial_o_at(h, splits, 0);
+    const float* pml = ws + partial_ml_at(n_q, h, splits, 0);
     if (splits <= kWave) {
-        r = merge_splits_small([p](uint32_t i) { return p[i]; }, splits, d, lane);
-    } else {
-        __shared__ float cw[kMaxMergeSplits];
-        __shared__ float red[2];
-        float m = -__builtin_inff();
-        for (int s = d; s < splits; s += HD) m = fmaxf(m, p[s * kRow]);
-        m = block_reduce<2>(m, OpMax{}, red);
-        __syncthreads();
-        float l = 0.0f;
-        for (int s = d; s < splits; s += HD) {
-            const float ls = p[s * kRow + 1];
-            const float c = ls == 0.0f ? 0.0f : exp2_hw(p[s * kRow] - m);
-            cw[s] = c;
-            l += ls * c;
-        }
-        l = block_reduce<2>(l, OpAdd{}, red);  // its barrier also publishes cw[]
-        float o = 0.0f;
-        constexpr int kBatch = 8;
-        for (int s0 = 0; s0 < splits; s0 += kBatch) {
-            float v[kBatch];
-#pragma unroll
-            for (int b = 0; b < kBatch; ++b) v[b] = p[(s0 + b < splits ? s0 + b : s0) * kRow + 2 + d];
-#pragma unroll
-            for (int b = 0; b < kBatch; ++b)
-                if (s0 + b < splits) o = __builtin_fmaf(cw[s0 + b], v[b], o);
-        }
-        r = l == 0.0f ? 0.0f : o / l;
+        const int half = threadIdx.x / kWave;
+        write_head_half(out, out16, h, half, lane, merge_head_half<0>(po, pml, splits, half, lane));
+        return;
     }
+    __shared__ float cw[kMaxMergeSplits];
+    __shared__ float red[2];
+    float m = -__builtin_inff();
+    for (int s = d; s < splits; s += HD) m = fmaxf(m, pml[2 * s]);
+    m = block_reduce<2>(m, OpMax{}, red);
+    __syncthreads();
+    float l = 0.0f;
+    for (int s = d; s < splits; s += HD) {
+        const float ls = pml[2 * s + 1];
+        const float c = ls == 0.0f ? 0.0f : exp2_hw(pml[2 * s] - m);
+        cw[s] = c;
+        l += ls * c;
+    }
+    l = block_reduce<2>(l, OpAdd{}, red);  // its barrier also publishes cw[]
+    float o = 0.0f;
+    constexpr int kBatch = 8;
+    for (int s0 = 0; s0 < splits; s0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) v[b] = po[static_cast<int64_t>(s0 + b < splits ? s0 + b : s0) * HD + d];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+            if (s0 + b < splits) o = __builtin_fmaf(cw[s0 + b], v[b], o);
+    }
+    const float r = l == 0.0f ? 0.0f : o / l;
     if (out) out[static_cast<int64_t>(h) * HD + d] = r;
     if (out16) out16[static_cast<int64_t>(h) * HD + d] = f32_to_f16_bits(r);
 }
@@ -603,6 +674,13 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
     const int group = n_q / n_kv;
     const int head_groups = (group + GT - 1) / GT;
     const int base_wg = n_kv * head_groups;
+    // The partials start at ws's first 16-byte boundary (128-bit merge loads).
+    if (ws) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(ws);
+        const uintptr_t up = (a + 15) & ~static_cast<uintptr_t>(15);
+        ws_floats -= static_cast<int64_t>((up - a) / sizeof(float));
+        ws = reinterpret_cast<float*>(up);
+    }
     // splits: enough workgroups to fill the GPU, at least one sub-chunk of
     // positions each, and no more partials than score_buf holds
     constexpr int kSubPositions = (kThreads / 16) * FENCE_ATTN_PPG;
@@ -625,7 +703,7 @@ int launch_split(float* out, uint16_t* out16, float* ws, const float* q, const u
     if (int st = launch(attn_split_kernel<GT, false, ROPE>, grid, dim3(kThreads), 0, s, out, out16, ws, q, kc, vc,
                         n_q, n_kv, seq_len, chunk, scale, qk, no_arrive))
         return st;
-    return launch(attn_merge_kernel, dim3(static_cast<unsigned>(n_q)), dim3(HD), 0, s, out, out16, ws,
+    return launch(attn_merge_kernel, dim3(static_cast<unsigned>(n_q)), dim3(HD), 0, s, out, out16, ws, n_q,
                   static_cast<int>(splits));
 }
 

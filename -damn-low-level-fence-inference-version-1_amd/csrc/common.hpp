@@ -11,6 +11,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <tuple>
+#include <type_traits>
 #include <utility>
 
 #include "fence/ops.h"
@@ -105,6 +106,7 @@ enum : int {
     kDppQuadXor2 = 0x4E,   // quad_perm [2,3,0,1]
     kDppHalfMirror = 0x141,// lane i <- lane 7-i within 8
     kDppMirror = 0x140,    // lane i <- lane 15-i within 16
+    kDppRowNewBcast0 = 0x150,  // + n: every lane <- lane n of its 16-lane row (row_newbcast:n)
 };
 
 // Every control used here permutes lanes inside a 16-lane row, so with all
@@ -119,6 +121,16 @@ __device__ __forceinline__ float dpp(float v) {
 // xor-16 exchange inside 32-lane halves (ds_swizzle bit mode: and=0x1F, xor=0x10)
 __device__ __forceinline__ float swz_xor16(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+// f(std::integral_constant<int, i>) for i = I .. N - 1: a loop whose index is
+// a compile-time constant in the body (DPP controls must be).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
 }
 
 __device__ __forceinline__ float readlane(float v, int lane) {
