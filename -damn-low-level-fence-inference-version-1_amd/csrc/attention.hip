@@ -93,6 +93,48 @@ struct QkIn {
     InvFreq tab;
 };
 
+// Reduce-scatter over the 16 lanes of a row: N values per lane in (N a power
+// of two, at most 16), and every lane leaves with the row's sum of one of
+// them, value idx(i) = sum over the halving steps s of bit (3 - s) of lane
+// i times N / 2^(s + 1).  Step s pairs lane i with lane i ^ 15, i ^ 7, i ^ 2,
+// i ^ 1 (DPP row_mirror, row_half_mirror, quad_perm xor 2, xor 1): the lane
+// whose step bit is 0 keeps the lower half of its values and adds its
+// partner's lower half, the other the upper halves; once one value is left a
+// step just adds the partner's.  All 64 lanes must be active.
+template <int S, int M>
+__device__ __forceinline__ float row_reduce_scatter(const float* v, int sl) {
+    if constexpr (S == 4) {
+        static_assert(M == 1, "at most 16 values");
+        return v[0];
+    } else {
+        constexpr int kCtrl = S == 0 ? kDppMirror : S == 1 ? kDppHalfMirror : S == 2 ? kDppQuadXor2 : kDppQuadXor1;
+        if constexpr (M == 1) {
+            const float w = v[0] + dpp<kCtrl>(v[0]);
+            return row_reduce_scatter<S + 1, 1>(&w, sl);
+        } else {
+            constexpr int H = M / 2;
+            const bool upper = (sl >> (3 - S)) & 1;
+            float w[H];
+#pragma unroll
+            for (int k = 0; k < H; ++k) {
+                const float keep = upper ? v[k + H] : v[k];
+                const float send = upper ? v[k] : v[k + H];
+                w[k] = keep + dpp<kCtrl>(send);
+            }
+            return row_reduce_scatter<S + 1, H>(w, sl);
+        }
+    }
+}
+
+// The index of the value row_reduce_scatter<0, N> leaves in lane sl.
+template <int N>
+__device__ __forceinline__ int row_scatter_index(int sl) {
+    int idx = 0;
+#pragma unroll
+    for (int s = 0, h = N / 2; h >= 1; ++s, h /= 2) idx += ((sl >> (3 - s)) & 1) * h;
+    return idx;
+}
+
 // Split partials in ws (16-byte aligned), n_q * splits * (128 + 2) floats:
 // the o rows [n_q][splits][128], then the (m, l) pairs [n_q][splits][2].
 constexpr int kHD = 128;
@@ -332,8 +374,14 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         // (position 0) or hold any bits; its weight is 0, and so is its V.
 #pragma unroll
         for (int i = 0; i < kPPG; ++i) vr[i] = on[i] ? vr[i] : h8(0);
-        // (A) scores, in log2 units
+        // (A) scores, in log2 units: each lane's 8-dim partial dots of its
+        // kPPG positions and GT heads, then one reduce-scatter over the row,
+        // after which lane sl holds the score of (position, head) index
+        // row_scatter_index(sl) and the first lane of each pair writes it
         float(&spb)[GT][kSub] = sp[sub & 1];
+        constexpr int kDots = kPPG * GT;  // index i * GT + g
+        static_assert(kDots <= 16 && (kDots & (kDots - 1)) == 0, "scores per row: a power of two, at most 16");
+        float dots[kDots];
 #pragma unroll
         for (int i = 0; i < kPPG; ++i) {
             float kf[8];
@@ -344,9 +392,15 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
                 float d = 0.0f;
 #pragma unroll
                 for (int k = 0; k < 8; ++k) d = __builtin_fmaf(qv[g][k], kf[k], d);
-                d = group_reduce<16>(d, OpAdd{});
-                if (sl == 0) spb[g][pg + kPG * i] = on[i] ? d * scale2 : -__builtin_inff();
+                dots[i * GT + g] = d;
             }
+        }
+        {
+            const float d = row_reduce_scatter<0, kDots>(dots, sl);
+            const int idx = row_scatter_index<kDots>(sl);
+            const int i = idx / GT, g = idx % GT;
+            constexpr int kCopies = 16 / kDots;  // lanes holding each score
+            if (sl % kCopies == 0) spb[g][pg + kPG * i] = t0 + pg + kPG * i < t_end ? d * scale2 : -__builtin_inff();
         }
         // One barrier per sub-chunk: the next sub-chunk writes the other
         // buffer, and the one after that comes after the next barrier.
@@ -354,41 +408,45 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(float* __restrict_
         // (B) every wave, every head: lane t holds position t0 + t -- the
         // sub-chunk's maximum, the weights and their sum, each computed the
         // same way in every wave, so all waves keep the same running values
-        float pw[GT], cw[GT];
+        float pw[GT], cw[GT], sv[GT], mx[GT], sm[GT];
+#pragma unroll
+        for (int g = 0; g < GT; ++g) sv[g] = spb[g][lane];
+#pragma unroll
+        for (int g = 0; g < GT; ++g) mx[g] = wave_reduce(fmaxf(-__builtin_inff(), sv[g]), OpMax{});
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
-            const float sv = spb[g][lane];
-            const float m = wave_reduce(fmaxf(-__builtin_inff(), sv), OpMax{});
-            const float mo = hm[g];
-            const float mn = fmaxf(mo, m);
-            const float p = sv == -__builtin_inff() ? 0.0f : exp2_hw(sv - mn);
-            float l = 0.0f;
-            l += p;
-            l = wave_reduce(l, OpAdd{});
-            const float c = hl[g] == 0.0f ? 0.0f : exp2_hw(mo - mn);  // nothing seen yet: no old weight
-            hl[g] = hl[g] * c + l;
+            const float mn = fmaxf(hm[g], mx[g]);
+            pw[g] = sv[g] == -__builtin_inff() ? 0.0f : exp2_hw(sv[g] - mn);
+            cw[g] = hl[g] == 0.0f ? 0.0f : exp2_hw(hm[g] - mn);  // nothing seen yet: no old weight
             hm[g] = mn;
-            cw[g] = c;
-            pw[g] = p;
         }
-        // (C) o = o * c + sum_t p_t v_t over the lane's dims; p_t from lane t
+#pragma unroll
+        for (int g = 0; g < GT; ++g) sm[g] = wave_reduce(pw[g], OpAdd{});
+#pragma unroll
+        for (int g = 0; g < GT; ++g) hl[g] = hl[g] * cw[g] + sm[g];
+        // (C) o = o * c + sum_t p_t v_t over the lane's dims.  Lane (row,
+        // i) takes p of its row's position i (pg + kPG i, from lane t of (B)),
+        // then step i broadcasts it over the row (DPP row_newbcast).
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) o[g][k] *= cw[g];
         }
+        float pq[GT];
 #pragma unroll
-        for (int i = 0; i < kPPG; ++i) {
+        for (int g = 0; g < GT; ++g) pq[g] = __shfl(pw[g], pg + kPG * (sl % kPPG), kWave);
+        static_for<0, kPPG>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
             float vf[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) vf[k] = static_cast<float>(vr[i][k]);
 #pragma unroll
             for (int g = 0; g < GT; ++g) {
-                const float p = __shfl(pw[g], pg + kPG * i, kWave);
+                const float p = dpp<kDppRowNewBcast0 + i>(pq[g]);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) o[g][k] = __builtin_fmaf(p, vf[k], o[g][k]);
             }
-        }
+        });
         ++sub;
     };
 
