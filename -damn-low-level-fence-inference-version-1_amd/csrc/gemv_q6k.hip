@@ -832,8 +832,11 @@ __global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENC
         load_seg(job.W[0], a0, nch, chg);
         load_seg(job.W[1], a0, nch, chu);
     };
-    // The first row's chunks go out before anything else waits.
-    if (o0 < n_out) load_row(o0);
+    // The first row's chunks go out before anything else waits, whether or
+    // not the wave has a row (load_row clamps to the last): with no branch
+    // around them the prologue's waits count them exactly and leave them in
+    // flight.
+    load_row(o0);
     if constexpr (NORM != 0) {
         const int nvw = rin.T / kWave;
         const bool has_res = rin.res != nullptr;
