@@ -270,9 +270,12 @@ __host__ __device__ constexpr int q6_wpr(int nb) {
 }
 __host__ __device__ constexpr int q6_passes(int nb) { return (nb + 4 * q6_wpr(nb) - 1) / (4 * q6_wpr(nb)); }
 
+// The lane's x pairs of every pass (binary16 zeros for a masked block).
+// Loads only: load_x_bias then forms the column biases, so loads issued in
+// between stay in flight while the biases wait for x.
 template <int PASSES>
-__device__ __forceinline__ void load_x(uint32_t (&xh)[PASSES][8], float (&kb)[PASSES][4], const uint16_t* x16,
-                                       int b0, int b1, int bslot, int h, int j) {
+__device__ __forceinline__ void load_x_pairs(uint32_t (&xh)[PASSES][8], const uint16_t* x16, int b0, int b1,
+                                             int bslot, int h, int j) {
     const bool vec = (reinterpret_cast<uintptr_t>(x16) & 7) == 0;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
@@ -292,9 +295,23 @@ __device__ __forceinline__ void load_x(uint32_t (&xh)[PASSES][8], float (&kb)[PA
             }
             xh[p][2 * c] = on ? lo : 0u;  // binary16 zeros: a masked block adds 0
             xh[p][2 * c + 1] = on ? hi : 0u;
-            kb[p][c] = q6_col_bias(xh[p][2 * c], xh[p][2 * c + 1]);
         }
     }
+}
+
+template <int PASSES>
+__device__ __forceinline__ void load_x_bias(const uint32_t (&xh)[PASSES][8], float (&kb)[PASSES][4]) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kb[p][c] = q6_col_bias(xh[p][2 * c], xh[p][2 * c + 1]);
+}
+
+template <int PASSES>
+__device__ __forceinline__ void load_x(uint32_t (&xh)[PASSES][8], float (&kb)[PASSES][4], const uint16_t* x16,
+                                       int b0, int b1, int bslot, int h, int j) {
+    load_x_pairs<PASSES>(xh, x16, b0, b1, bslot, h, j);
+    load_x_bias<PASSES>(xh, kb);
 }
 
 // A launch's matrices: up to kMaxMats row blocks that share x and K, their
@@ -421,7 +438,7 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
 
     uint32_t xh[PASSES][8];
     float kb[PASSES][4];
-    if constexpr (!NORM) load_x<PASSES>(xh, kb, x16, b0, b1, bslot, h, j);
+    if constexpr (!NORM) load_x_pairs<PASSES>(xh, x16, b0, b1, bslot, h, j);  // biases once the first group is out
 
     // NORM, first half: the row's loads, issued before the first group's
     // blocks.  Wave w holds the row norm's waves w, w + NW, ... (vw < T / 64);
@@ -672,22 +689,25 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
             __syncthreads();  // red[] is rewritten by the next group
         }
     };
-    if constexpr (PF) {  // the first group's chunks here (NORM: in the prologue), every later one's a group ahead
-        if constexpr (NORM == 0) {
-            int64_t o, lr, a0;
-            int m, nch;
-            uint32_t delta;
-            row_of(blockIdx.x, &o, &m, &lr);
-            seg_of(lr, &a0, &nch, &delta);
-            load_seg(job.W[m], a0, nch, ch);
-        }
+    // The first group's chunks (NORM: loaded in the prologue) go out right
+    // behind x's loads, unconditionally (row_of clamps), so the column
+    // biases wait for x alone and the chunks stay in flight meanwhile.
+    if constexpr (NORM == 0) {
+        int64_t o, lr, a0;
+        int m, nch;
+        uint32_t delta;
+        row_of(blockIdx.x, &o, &m, &lr);
+        seg_of(lr, &a0, &nch, &delta);
+        load_seg(job.W[m], a0, nch, ch);
+        __builtin_amdgcn_sched_barrier(0);
+        load_x_bias<PASSES>(xh, kb);
+    }
+    if constexpr (PF) {  // every later group's chunks a group ahead
         for (int64_t g = blockIdx.x; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::true_type{});
     } else {
         int64_t g = blockIdx.x;
-        if constexpr (NORM != 0) {
-            run_group(g, std::true_type{});  // g < the group count: the grid is at most that
-            g += gridDim.x;
-        }
+        if (g * kOutPerGroup < n_out) run_group(g, std::true_type{});  // workgroup-uniform
+        g += gridDim.x;
         for (; g * kOutPerGroup < n_out; g += gridDim.x) run_group(g, std::false_type{});
     }
     if constexpr (CLOCK)
