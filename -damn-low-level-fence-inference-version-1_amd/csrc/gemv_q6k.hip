@@ -98,6 +98,12 @@ static_assert(FENCE_GEMV_Q6K_PAIRW == 0 || FENCE_GEMV_Q6K_PAIRW == 4 || FENCE_GE
 #ifndef FENCE_GEMV_Q6K_PAIRW_WPE
 #define FENCE_GEMV_Q6K_PAIRW_WPE 4
 #endif
+// 1: rows whose last pass holds two blocks (nb % 4 == 2) share that pass
+// between gate and up in the one-wave pair kernel (MERGE there); 0: each row
+// its own.  Same results, bit for bit.
+#ifndef FENCE_GEMV_Q6K_PAIRW_MERGE
+#define FENCE_GEMV_Q6K_PAIRW_MERGE 1
+#endif
 // 1: the one-wave pair kernel loads the next output row while the current
 // one is computed; 0: each row after the previous one.
 #ifndef FENCE_GEMV_Q6K_PAIRW_PF
@@ -728,9 +734,16 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
 // is computed.  NORM / VW: the staged kernel's prologue (RmsIn), for NW waves.
 // CLOCK: the instrumented copy (FENCE_WAVE_CLOCK builds), whose row-group
 // count is the wave's rows.
-template <int PASSES, int NW, int NORM, int VW, bool PF, bool CLOCK = false>
+// MERGE (rows whose last pass holds two blocks, nb % 4 == 2): that pass is
+// one pass for both rows -- block slots 0, 1 take gate's two blocks, slots
+// 2, 3 up's -- and up's two values move to slots 0, 1 (a half-wave swap),
+// where the unmerged layout computes them: each lane adds exactly the values
+// it adds there, in the same order, so the sums are the same bits, from five
+// passes per output row instead of six.
+template <int PASSES, int NW, int NORM, int VW, bool PF, bool MERGE, bool CLOCK = false>
 __global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENCE_GEMV_Q6K_PAIRW_WPE))) void gemv_q6k_pairw_kernel(const Q6Job job, const uint16_t* __restrict__ x16,
                                                                   int nb, const RmsIn rin) {
+    static_assert(!MERGE || PASSES >= 2, "a merged last pass follows full ones");
     constexpr int kSegBytes = 4 * PASSES * kBlockBytes + 32;  // + alignment slack
     constexpr int kBufBytes = (kSegBytes + 15) / 16 * 16;
     constexpr int kChunkSlots = (kSegBytes / 16 + kWave - 1) / kWave;
@@ -754,7 +767,15 @@ __global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENC
 
     uint32_t xh[PASSES][8];
     float kb[PASSES][4];
-    if constexpr (!NORM) load_x<PASSES>(xh, kb, x16, b0, b1, bslot, h, j);
+    // MERGE: x of the merged pass's block, 4 (PASSES - 1) + (bslot & 1), for
+    // every slot (the last pass of xh masks slots 2, 3)
+    uint32_t xm[1][8];
+    float km[1][4];
+    const int b0m = 4 * (PASSES - 1) + (bslot & 1) - bslot;
+    if constexpr (!NORM) {
+        load_x<PASSES>(xh, kb, x16, b0, b1, bslot, h, j);
+        if constexpr (MERGE) load_x<1>(xm, km, x16, b0m, b1, bslot, h, j);
+    }
 
     static_assert(NORM == 0 || (VW >= 1 && VW * NW <= 16 + NW - 1), "VW: 1 .. ceil(16 / NW) slots");
     constexpr int kVW = NORM ? VW : 1;
@@ -816,28 +837,33 @@ __global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENC
             *reinterpret_cast<u4*>(buf + dst) = ch[k];
         }
     };
-    // The lane's sum over the row staged in buf, in the staged kernel's order.
-    auto row_part = [&](const uint8_t* buf, uint32_t delta) {
-        const uint32_t base = delta + blk_off;
+    // The lane's value of the block staged at byte `base` of buf (pass offset
+    // included), against x pairs xp and biases kp.
+    auto block_value = [&](const uint8_t* buf, uint32_t base, const uint32_t* xp, const float* kp) {
         const uint32_t sh = base & 3u;
         const uint8_t* ab = buf + (base & ~3u);
         const uint8_t* bb = buf + base;
+        const uint32_t* wa = reinterpret_cast<const uint32_t*>(ab + lane_ql);
+        const uint32_t* wb = reinterpret_cast<const uint32_t*>(ab + lane_ql + 32);
+        const uint32_t* wc = reinterpret_cast<const uint32_t*>(ab + lane_qh);
+        const uint32_t a = __builtin_amdgcn_alignbyte(wa[1], wa[0], sh);
+        const uint32_t bq = __builtin_amdgcn_alignbyte(wb[1], wb[0], sh);
+        const uint32_t c = __builtin_amdgcn_alignbyte(wc[1], wc[0], sh);
+        const int8_t* scb = reinterpret_cast<const int8_t*>(bb + lane_sc);
+        int sc[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sc[q] = scb[2 * q];
+        const uint16_t dbits = *reinterpret_cast<const uint16_t*>(bb + 208);
+        const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+        return q6_lane_dot(q6_unpack(a, bq, c), xp, kp, sc, d);
+    };
+    // The lane's sum over the first NP passes of the row staged in buf, in
+    // the staged kernel's order.
+    auto row_part = [&](const uint8_t* buf, uint32_t delta, auto np) {
         float part = 0.0f;
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const uint32_t* wa = reinterpret_cast<const uint32_t*>(ab + p * kPassBytes + lane_ql);
-            const uint32_t* wb = reinterpret_cast<const uint32_t*>(ab + p * kPassBytes + lane_ql + 32);
-            const uint32_t* wc = reinterpret_cast<const uint32_t*>(ab + p * kPassBytes + lane_qh);
-            const uint32_t a = __builtin_amdgcn_alignbyte(wa[1], wa[0], sh);
-            const uint32_t bq = __builtin_amdgcn_alignbyte(wb[1], wb[0], sh);
-            const uint32_t c = __builtin_amdgcn_alignbyte(wc[1], wc[0], sh);
-            const int8_t* scb = reinterpret_cast<const int8_t*>(bb + p * kPassBytes + lane_sc);
-            int sc[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) sc[q] = scb[2 * q];
-            const uint16_t dbits = *reinterpret_cast<const uint16_t*>(bb + p * kPassBytes + 208);
-            const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
-            const float v = q6_lane_dot(q6_unpack(a, bq, c), xh[p], kb[p], sc, d);
+        for (int p = 0; p < decltype(np)::value; ++p) {
+            const float v = block_value(buf, delta + blk_off + p * kPassBytes, xh[p], kb[p]);
             part += on[p] ? v : 0.0f;
         }
         return part;
@@ -905,6 +931,7 @@ __global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENC
         }
         __syncthreads();
         load_x<PASSES>(xh, kb, xs, b0, b1, bslot, h, j);
+        if constexpr (MERGE) load_x<1>(xm, km, xs, b0m, b1, bslot, h, j);
         __syncthreads();  // lds holds staged rows from here on
     }
     for (int64_t o = o0; o < n_out; o += waves) {  // wave-uniform
@@ -922,8 +949,24 @@ __global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENC
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        const float gs = wave_sum(row_part(bufg, delta));
-        const float us = wave_sum(row_part(bufu, delta));
+        float gs, us;
+        if constexpr (MERGE) {
+            using Full = std::integral_constant<int, PASSES - 1>;
+            const float gp = row_part(bufg, delta, Full{});
+            const float up = row_part(bufu, delta, Full{});
+            // the merged pass: slots 0, 1 gate's blocks, slots 2, 3 up's
+            const float vm = block_value(bslot < 2 ? bufg : bufu,
+                                         delta + (bslot & 1) * kBlockBytes + (PASSES - 1) * kPassBytes, xm[0], km[0]);
+            // up's values to slots 0, 1: y's lower half takes x's upper half
+            float x = vm, y = vm;
+            asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+            gs = wave_sum(gp + (bslot < 2 ? vm : 0.0f));
+            us = wave_sum(up + (bslot < 2 ? y : 0.0f));
+        } else {
+            using All = std::integral_constant<int, PASSES>;
+            gs = wave_sum(row_part(bufg, delta, All{}));
+            us = wave_sum(row_part(bufu, delta, All{}));
+        }
         if (lane == 0) {
             const float act = silu_mul(gs, us);
             job.act16[o] = f32_to_f16_bits(act);
@@ -1085,8 +1128,16 @@ int launch_pairw_vw(const Q6Job& job, int64_t n_out, const uint16_t* x, int nb, 
     constexpr int nw = FENCE_GEMV_Q6K_PAIRW > 0 ? FENCE_GEMV_Q6K_PAIRW : 4;
     static std::atomic<int> cache[64];
     constexpr bool pf = FENCE_GEMV_Q6K_PAIRW_PF != 0;
-    return launch_grid_as(gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, false>,
-                          gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, FENCE_WAVE_CLOCK != 0>, kWave * nw, cache,
+    if constexpr (PASSES >= 2 && FENCE_GEMV_Q6K_PAIRW_MERGE) {
+        if (nb % 4 == 2) {
+            static std::atomic<int> mcache[64];
+            return launch_grid_as(gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, true, false>,
+                                  gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, true, FENCE_WAVE_CLOCK != 0>,
+                                  kWave * nw, mcache, (n_out + nw - 1) / nw, s, job, x, nb, rin);
+        }
+    }
+    return launch_grid_as(gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, false, false>,
+                          gemv_q6k_pairw_kernel<PASSES, nw, NORM, VW, pf, false, FENCE_WAVE_CLOCK != 0>, kWave * nw, cache,
                           (n_out + nw - 1) / nw, s, job, x, nb, rin);
 }
 

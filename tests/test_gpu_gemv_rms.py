@@ -183,7 +183,7 @@ def test_swiglu_rms_equals_norm_then_pair(M, K):
 # norm launch followed by the pair launch on its binary16 row.
 @pytest.mark.parametrize("nb,M,residual", [
     (1, 8, True), (3, 8, False), (4, 2, True), (8, 1, True), (9, 8, False), (13, 8, True),
-    (16, 3, True), (10, 4100, False),
+    (16, 3, True), (10, 4100, False), (6, 8, True), (10, 4, True), (14, 4, False),
 ])
 def test_swiglu_rms_one_wave_pair_edges(nb, M, residual):
     K = 256 * nb

@@ -339,13 +339,15 @@ def test_gemv_q6k_swiglu_equals_unfused_sequence(oracle, M, K):
 
 # Gate/up pairs of rows of at most 16 blocks take the kernel with one wave per
 # output row (8-wave workgroups, the next row prefetched): every pass count
-# (1-4 passes of four blocks), masked block slots, fewer rows than a
+# (1-4 passes of four blocks), masked block slots, a last pass of two blocks
+# shared by gate and up (nb = 6, 10, 14), fewer rows than a
 # workgroup's waves, exactly one workgroup's, and row counts either side of
 # the resident grid's waves, each bit-equal to the two GEMV launches and the
 # SwiGLU launch it replaces.  (M * nb % 8 == 0 keeps them on the staged path.)
 @pytest.mark.parametrize("nb,M", [
     (1, 8), (1, 64), (2, 4), (3, 8), (4, 2), (5, 8), (8, 1), (8, 7), (8, 9),
     (9, 8), (12, 6), (13, 8), (16, 1), (16, 3), (16, 8), (10, 4092), (10, 4100), (10, 8196),
+    (6, 8), (10, 4), (14, 4), (14, 1028),
 ])
 def test_gemv_q6k_swiglu_one_wave_pair_edges(nb, M):
     K = 256 * nb
