@@ -132,7 +132,7 @@ def test_gemv_q6k_bias(oracle):
     assert_close(got, ref, abs_scale(W, x, K), "q6k bias", slack=2.0 ** -23 * np.abs(ref))
 
 
-@pytest.mark.parametrize("nb", [13, 16, 17, 21, 24, 27, 32, 33, 40, 48, 49, 60, 64, 65, 70])
+@pytest.mark.parametrize("nb", [6, 10, 13, 14, 16, 17, 21, 24, 27, 32, 33, 40, 48, 49, 60, 64, 65, 70])
 def test_direct_kernel_sums_in_the_staged_order(nb):
     """The direct kernel (weights only 2-byte aligned) must give every row the
     staged kernel's bits: rows of more than 16 blocks are summed per segment
@@ -149,6 +149,34 @@ def test_direct_kernel_sums_in_the_staged_order(nb):
     LIVE.extend([raw, y])
     F.gemv_q6k(raw.data_ptr() + 2, dev(x.view(np.int16)).data_ptr(), y.data_ptr(), M, K, stream())
     assert np.array_equal(host(y).view(np.uint32), staged.view(np.uint32)), "direct differs from staged"
+
+
+# Multi launches of rows whose last pass holds two blocks (6, 10, 14), small
+# and empty matrices among them, biases on some: each row must have the bits
+# the direct kernel (2-byte aligned copies of the same matrices) gives it,
+# its bias included, and only its own output may be written.
+@pytest.mark.parametrize("shapes,nb", [((4, 12, 8), 10), ((8,), 10), ((4,), 6), ((12, 4), 14), ((4096, 1024, 1024), 10),
+                                       ((1028, 4, 0, 8), 10)])
+def test_multi_rows_equal_the_direct_kernel(oracle, shapes, nb):
+    torch = torch_mod()
+    K = 256 * nb
+    rng = np.random.default_rng(sum(shapes) + nb)
+    Ws = [make_q6k_matrix(rng, M, K) if M else np.zeros((0, nb * 210), np.uint8) for M in shapes]
+    bs = [rng.standard_normal(M).astype(np.float32) if i % 2 == 0 else None for i, M in enumerate(shapes)]
+    x = rand_x(rng, K)
+    got = run_q6k_multi([W if W.size else None for W in Ws], x, list(shapes), K, bs)
+    for i, (W, M) in enumerate(zip(Ws, shapes)):
+        if M == 0:
+            continue
+        raw = torch.zeros(W.size + 16, dtype=torch.uint8, device="cuda")
+        raw[2:2 + W.size] = dev(W.reshape(-1))
+        y = torch.full((M,), float("nan"), dtype=torch.float32, device="cuda")
+        LIVE.extend([raw, y])
+        F.gemv_q6k(raw.data_ptr() + 2, dev(x.view(np.int16)).data_ptr(), y.data_ptr(), M, K, stream())
+        ref = host(y) + (bs[i] if bs[i] is not None else 0)
+        assert np.array_equal(got[i].view(np.uint32), ref.astype(np.float32).view(np.uint32)), f"matrix {i}"
+        assert_close(got[i] - (bs[i] if bs[i] is not None else 0), oracle.gemv_q6k(W, x), abs_scale(W, x, K),
+                     f"two-row {i}")
 
 
 @pytest.mark.parametrize("shapes,K", [((176, 73, 25, 103), 6912), ((248, 5), 5376), ((80, 139, 79), 9984),
