@@ -192,14 +192,28 @@ struct Q6Lane {
     uint32_t w[4];
 };
 
+// Every byte of c holds column 0's high bits in bits 0-1, column 1's in
+// 2-3, column 2's in 4-5 and column 3's in 6-7.  ce keeps columns 0 and 2
+// (bits 0-1, 4-5), co columns 1 and 3 moved to the same places; each
+// column's byte is then one bit-field insert, (nibble & 0x0F) | (bits above
+// 0x0F of the crumb word), whose bits 6-7 are clear.  Written as asm: the
+// compiler folds the masks back into its own three-operation form.
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {  // (x & m) | (y & ~m)
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(x), "v"(y));
+    return r;
+}
+
 __device__ __forceinline__ Q6Lane q6_unpack(uint32_t a, uint32_t b, uint32_t c) {
-    constexpr uint32_t kNib = 0x0F0F0F0Fu;    // low nibble of every byte
-    constexpr uint32_t kCrumb = 0x30303030u;  // bits 4..5: the high two bits
+    constexpr uint32_t kNib = 0x0F0F0F0Fu;  // low nibble of every byte
+    constexpr uint32_t kTwo = 0x33333333u;  // bits 0-1 and 4-5 of every byte
+    const uint32_t ce = c & kTwo;
+    const uint32_t co = (c >> 2) & kTwo;
     Q6Lane r;
-    r.w[0] = (a & kNib) | ((c << 4) & kCrumb);
-    r.w[1] = (b & kNib) | ((c << 2) & kCrumb);
-    r.w[2] = ((a >> 4) & kNib) | (c & kCrumb);
-    r.w[3] = ((b >> 4) & kNib) | ((c >> 2) & kCrumb);
+    r.w[0] = bfi(kNib, a, ce << 4);
+    r.w[1] = bfi(kNib, b, co << 4);
+    r.w[2] = bfi(kNib, a >> 4, ce);
+    r.w[3] = bfi(kNib, b >> 4, co);
     return r;
 }
 
@@ -239,8 +253,12 @@ __device__ __forceinline__ float dot2_f16(h2 a, h2 b, float c) {
     return d;
 }
 
+// d * acc is one v_fma_mix_f32 with the binary16 d as its operand and 0
+// added: the product's value, rounded once, except that a zero product is
+// +0 whatever its sign (the lane values are only added, and a +0 in place
+// of a -0 changes no nonzero sum).
 __device__ __forceinline__ float q6_lane_dot(const Q6Lane& q, const uint32_t* xh, const float* kb, const int* sc,
-                                             float d) {
+                                             _Float16 d) {
 #pragma clang fp contract(off)
     float acc = 0.0f;
 #pragma unroll
@@ -249,7 +267,9 @@ __device__ __forceinline__ float q6_lane_dot(const Q6Lane& q, const uint32_t* xh
         p = __builtin_amdgcn_fdot2(q6_pair(q.w[c], 0x00070006u), __builtin_bit_cast(h2, xh[2 * c + 1]), p, false);
         acc = __builtin_fmaf(static_cast<float>(sc[c]), p, acc);
     }
-    return d * acc;
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(d), "v"(acc));
+    return r;
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return wave_reduce(v, OpAdd{}); }
@@ -642,7 +662,7 @@ __global__ __launch_bounds__((kWave * staged_waves<WPR, PAIR, NORM>())) void gem
 #pragma unroll
                 for (int q = 0; q < 4; ++q) sc[q] = scb[2 * q];
                 const uint16_t dbits = *reinterpret_cast<const uint16_t*>(bb + p * kPassBytes + 208);
-                const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+                const _Float16 d = __builtin_bit_cast(_Float16, dbits);
                 const float v = q6_lane_dot(q6_unpack(a, bq, c), xh[p], kb[p], sc, d);
                 if constexpr (XW) xr[wid][p][lane] = on[p] ? v : 0.0f;
                 else part += on[p] ? v : 0.0f;
@@ -854,17 +874,19 @@ __global__ __launch_bounds__(kWave * NW) __attribute__((amdgpu_waves_per_eu(FENC
 #pragma unroll
         for (int q = 0; q < 4; ++q) sc[q] = scb[2 * q];
         const uint16_t dbits = *reinterpret_cast<const uint16_t*>(bb + 208);
-        const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+        const _Float16 d = __builtin_bit_cast(_Float16, dbits);
         return q6_lane_dot(q6_unpack(a, bq, c), xp, kp, sc, d);
     };
     // The lane's sum over the first NP passes of the row staged in buf, in
-    // the staged kernel's order.
+    // the staged kernel's order.  MERGE's first PASSES - 1 passes hold four
+    // blocks each: no slot is masked there.
     auto row_part = [&](const uint8_t* buf, uint32_t delta, auto np) {
+        constexpr bool kFull = MERGE && decltype(np)::value < PASSES;
         float part = 0.0f;
 #pragma unroll
         for (int p = 0; p < decltype(np)::value; ++p) {
             const float v = block_value(buf, delta + blk_off + p * kPassBytes, xh[p], kb[p]);
-            part += on[p] ? v : 0.0f;
+            part += kFull || on[p] ? v : 0.0f;
         }
         return part;
     };
@@ -1004,7 +1026,7 @@ __device__ __forceinline__ float direct_block(const uint8_t* Wm, const uint16_t*
     float kbc[4];
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) kbc[cc] = q6_col_bias(xh[2 * cc], xh[2 * cc + 1]);
-    const float d = static_cast<float>(__builtin_bit_cast(_Float16, dbits));
+    const _Float16 d = __builtin_bit_cast(_Float16, dbits);
     return q6_lane_dot(q6_unpack(a, bq, c), xh, kbc, sc, d);
 }
 
