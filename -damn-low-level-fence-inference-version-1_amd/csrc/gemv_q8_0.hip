@@ -203,14 +203,32 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_staged_kernel(float* _
             ch[c] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(row + off));
         }
     };
-    u4 ch[kChunkSlots];
-    if constexpr (PREFETCH) load_row(wave, ch);
-
     // x passes through LDS once per workgroup (the row buffers, 4 * 34K/32
     // bytes, hold its 4K bytes), so each wave reads its quarters' x from LDS
-    // instead of issuing its own strided global loads.
+    // instead of issuing its own strided global loads.  Aligned x: each lane
+    // issues its float4 loads (up to kXSlots) before the first row's and
+    // stores them once they arrive, so the row's loads stay in flight (gfx9
+    // retires loads in issue order) and no lane waits for a load per store.
     float* xl = reinterpret_cast<float*>(row_lds);
-    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    constexpr int kXSlots = 4;
+    const bool xvec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (K >> 2) <= kXSlots * kGemvThreads;
+    f4 xv[kXSlots];
+    if (xvec) {  // workgroup-uniform
+#pragma unroll
+        for (int k = 0; k < kXSlots; ++k) {
+            const int i = threadIdx.x + k * kGemvThreads;
+            xv[k] = reinterpret_cast<const f4*>(x)[i < (K >> 2) ? i : 0];
+        }
+    }
+    u4 ch[kChunkSlots];
+    if constexpr (PREFETCH) load_row(wave, ch);
+    if (xvec) {
+#pragma unroll
+        for (int k = 0; k < kXSlots; ++k) {
+            const int i = threadIdx.x + k * kGemvThreads;
+            if (i < (K >> 2)) reinterpret_cast<f4*>(xl)[i] = xv[k];
+        }
+    } else if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
         for (int i = threadIdx.x; i < (K >> 2); i += kGemvThreads)
             reinterpret_cast<f4*>(xl)[i] = reinterpret_cast<const f4*>(x)[i];
     } else {

@@ -438,7 +438,7 @@ bool Qwen3Model::forward_reference(int token_id, int pos) {
 // rest still read the old one.  q, k and v are one launch; attention applies
 // QK-norm and RoPE to q itself, prepares and stores the new k and v row, and
 // writes the binary16 input of the o projection; gate, up and SwiGLU are one
-// launch (writing act_half).  6 calls per layer instead of 22 plus two
+// launch (writing act_half).  5 calls per layer instead of 22 plus two
 // copies; every result is bit-identical to the reference sequence's.
 bool Qwen3Model::forward_fused(int token_id, int pos) {
     const Qwen3Config& c = config;
