@@ -9,6 +9,8 @@
 //                                      in-place form, RoPE's traffic)
 //   a == null: out[i] = 0             (1 write: the masked half of the
 //                                      causal softmax's output)
+//   fence_calib_read: sums[w] = the sum of what wave w read (1 read: a
+//                     GEMV's weight stream; one float written per wave)
 //
 // Each lane moves VPT float4s of every stream with non-temporal 128-bit loads
 // and stores (the elementwise kernels' memory access), THREADS lanes per
@@ -41,6 +43,26 @@ __global__ __launch_bounds__(THREADS) void calib_stream_kernel(float* out, const
     }
 }
 
+// Read-only: each lane adds the components of its VPT float4s, and lane 0
+// of each wave stores the wave's sum, so no load can be dropped and the
+// writes are 4 bytes per 1,024 * VPT read.
+template <int THREADS, int VPT>
+__global__ __launch_bounds__(THREADS) void calib_read_kernel(float* sums, const float* a, int64_t n4) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (THREADS * VPT) + threadIdx.x;
+    f4 v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t i = base + static_cast<int64_t>(j) * THREADS;
+        v[j] = i < n4 ? ld4<true>(a + 4 * i) : f4(0.0f);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) acc += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    acc = wave_reduce(acc, OpAdd{});
+    if ((threadIdx.x & (kWave - 1)) == 0)
+        sums[static_cast<int64_t>(blockIdx.x) * (THREADS / kWave) + threadIdx.x / kWave] = acc;
+}
+
 template <int THREADS, int VPT>
 int calib_launch(float* out, const float* a, const float* b, int64_t n4, hipStream_t s) {
     const unsigned grid = grid_1d(n4, THREADS * VPT);
@@ -55,6 +77,16 @@ int calib_vpt(int vpt, float* out, const float* a, const float* b, int64_t n4, h
         case 1: return calib_launch<THREADS, 1>(out, a, b, n4, s);
         case 2: return calib_launch<THREADS, 2>(out, a, b, n4, s);
         case 4: return calib_launch<THREADS, 4>(out, a, b, n4, s);
+        default: return FENCE_ERROR_INVALID_VALUE;
+    }
+}
+
+template <int THREADS>
+int calib_read_vpt(int vpt, float* sums, const float* a, int64_t n4, hipStream_t s) {
+    switch (vpt) {
+        case 1: return launch(calib_read_kernel<THREADS, 1>, dim3(grid_1d(n4, THREADS)), dim3(THREADS), 0, s, sums, a, n4);
+        case 2: return launch(calib_read_kernel<THREADS, 2>, dim3(grid_1d(n4, THREADS * 2)), dim3(THREADS), 0, s, sums, a, n4);
+        case 4: return launch(calib_read_kernel<THREADS, 4>, dim3(grid_1d(n4, THREADS * 4)), dim3(THREADS), 0, s, sums, a, n4);
         default: return FENCE_ERROR_INVALID_VALUE;
     }
 }
@@ -74,6 +106,19 @@ extern "C" int fence_calib_stream(float* out, const float* a, const float* b, in
     switch (threads) {
         case 64: return calib_vpt<64>(vpt, out, a, b, n4, stream);
         case 256: return calib_vpt<256>(vpt, out, a, b, n4, stream);
+        default: return FENCE_ERROR_INVALID_VALUE;
+    }
+}
+
+extern "C" int fence_calib_read(float* sums, const float* a, int64_t n, int threads, int vpt, hipStream_t stream) {
+    using namespace fence;
+    if (!sums || !a || n < 0 || n % 4 != 0 || !aligned(a, 16)) return FENCE_ERROR_INVALID_VALUE;
+    const int64_t n4 = n / 4;
+    if (n4 > kMaxLaunchLanes) return FENCE_ERROR_INVALID_VALUE;
+    if (n4 == 0) return FENCE_SUCCESS;
+    switch (threads) {
+        case 64: return calib_read_vpt<64>(vpt, sums, a, n4, stream);
+        case 256: return calib_read_vpt<256>(vpt, sums, a, n4, stream);
         default: return FENCE_ERROR_INVALID_VALUE;
     }
 }

@@ -168,8 +168,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_kernel(float* __restri
 // v_alignbyte.  One wave's LDS operations complete in order, so the next
 // row's writes cannot overtake this row's reads.  LDS: 4 * row_bytes + 16
 // bytes per workgroup; the 16 pad bytes take the unused third dword of the
-// last quarter and the stores of lanes past the row's last chunk.
-template <int SLOTS, bool FULL, bool PREFETCH>
+// last quarter and the stores of lanes past the row's last chunk.  PF rows
+// of loads are in flight while a row is computed (0: none; 2: two register
+// buffers, refilled alternately).
+template <int SLOTS, bool FULL, int PF>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_staged_kernel(float* __restrict__ y,
                                                                         const uint8_t* __restrict__ W,
                                                                         const float* __restrict__ x,
@@ -220,8 +222,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_staged_kernel(float* _
             xv[k] = reinterpret_cast<const f4*>(x)[i < (K >> 2) ? i : 0];
         }
     }
-    u4 ch[kChunkSlots];
-    if constexpr (PREFETCH) load_row(wave, ch);
+    u4 ch[PF > 1 ? 2 : 1][kChunkSlots];
+    if constexpr (PF > 0) load_row(wave, ch[0]);
+    if constexpr (PF > 1) load_row(wave + nwaves, ch[1]);
     if (xvec) {
 #pragma unroll
         for (int k = 0; k < kXSlots; ++k) {
@@ -253,8 +256,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_staged_kernel(float* _
     }
     __syncthreads();  // every wave has its x before any row overwrites the buffers
 
-    for (int r = wave; r < M; r += nwaves) {
-        if constexpr (!PREFETCH) load_row(r, ch);
+    auto row_step = [&](int r, u4* ch) {
+        if constexpr (PF == 0) load_row(r, ch);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < kChunkSlots; ++c) {
@@ -264,9 +267,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_staged_kernel(float* _
             uint8_t* dst = cc < nchunks ? buf + 16 * cc : pad;
             *reinterpret_cast<u4*>(dst) = ch[c];
         }
-        if constexpr (PREFETCH) {
-            // the next row's loads fly while this row is computed from LDS
-            load_row(r + nwaves, ch);
+        if constexpr (PF > 0) {
+            // the buffer's next row loads while this row is computed from LDS
+            load_row(r + PF * nwaves, ch);
             __builtin_amdgcn_sched_barrier(0);
         }
         float acc = 0.0f;
@@ -287,7 +290,21 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_staged_kernel(float* _
             else acc += on[s] ? c : 0.0f;
         }
         acc = wave_sum_of_quads(acc);
-        if (lane == 0) y[r] = acc;
+        // PF 2: every lane stores the (wave-uniform) sum, so no branch
+        // separates the two buffers' loads and each wait stays exact
+        if (PF > 1 || lane == 0) y[r] = acc;
+    };
+    if constexpr (PF < 2) {
+        for (int r = wave; r < M; r += nwaves) row_step(r, ch[0]);
+    } else {
+        // rows in pairs with no branch between them, so each wait leaves the
+        // other buffer's loads in flight; an odd last row after the loop
+        int r = wave;
+        for (; r + nwaves < M; r += 2 * nwaves) {
+            row_step(r, ch[0]);
+            row_step(r + nwaves, ch[1]);
+        }
+        if (r < M) row_step(r, ch[0]);
     }
 }
 
@@ -373,7 +390,7 @@ int launch_slots(float* y, const uint8_t* W, const float* x, int M, int K, hipSt
     const bool full = K == kWave * 8 * SLOTS;
     if (FENCE_GEMV_Q8_STAGED && K % 256 == 0 && aligned(W, 16)) {
         const size_t lds = static_cast<size_t>(kGemvThreads / kWave) * (K / 32) * 34 + 16;
-        constexpr bool pf = FENCE_GEMV_Q8_PREFETCH;
+        constexpr int pf = FENCE_GEMV_Q8_PREFETCH;
         if (full) return launch_rows(gemv_q8_0_staged_kernel<SLOTS, true, pf>, y, W, x, M, K, 1, lds, s);
         return launch_rows(gemv_q8_0_staged_kernel<SLOTS, false, pf>, y, W, x, M, K, 1, lds, s);
     }

@@ -76,6 +76,7 @@ SIGNATURES = {
     "fence_time_next_launch": (_P, _P),
     "fence_time_next_launches": (_P, _P, _I),
     "fence_calib_stream": (_P, _P, _P, _L, _I, _I, _P),
+    "fence_calib_read": (_P, _P, _L, _I, _I, _P),
     "fence_status_string": (_I,),
     "fence_version": (),
 }
@@ -332,6 +333,12 @@ def calib_stream(out, a, b, n, threads=64, vpt=1, stream=None) -> None:
     """Plain stream out = a + b (b given) or out = a (b None) for bandwidth
     calibration; see include/fence/ops.h."""
     _call("fence_calib_stream", out, a, b, n, threads, vpt, stream)
+
+
+def calib_read(sums, a, n, threads=64, vpt=1, stream=None) -> None:
+    """Read-only stream over a[0, n): wave w writes the sum it read to
+    sums[w]; see include/fence/ops.h."""
+    _call("fence_calib_read", sums, a, n, threads, vpt, stream)
 
 
 def rope_inv_freq(head_dim: int, freq_base: float):

@@ -467,6 +467,13 @@ def main():
             ceiling["step_GBps"] = step_ceiling_gbps({"softmax": cs, "swiglu": c2, "rope": c1})
             ceiling["step_source"] = "step bytes over the sum of each op's bytes at its mix's stream rate"
 
+    if "stream_1r" in ceiling and isinstance(lm_head, dict) and "GBps" in lm_head:
+        c = ceiling["stream_1r"]["GBps"]
+        lm_head["ceiling_GBps"] = c
+        lm_head["frac_of_ceiling"] = round(lm_head["GBps"] / c, 4)
+        lm_head["ceiling_source"] = "practical_ceiling.stream_1r (a plain read-only float4 stream over the " \
+                                    "table's bytes, same rotation)"
+
     cpu = None if args.no_cpu else section("cpu_baseline", lambda: cpu_baseline(args.cpu_seconds))
     cpu_all = None if args.no_cpu else section("cpu_baseline_all_cores",
                                                lambda: cpu_baseline_all_cores(args.cpu_seconds / 2))
@@ -1296,7 +1303,9 @@ def practical_ceiling(torch, F, reps):
       1 read + 1 write in place at RoPE's size, Q + K [8192 x 40 x 128];
       the causal softmax's bytes: 1 read + 1 write in place over its unmasked
       scores (32 x 2048 x 2049 / 2) and 1 write of zeros over the masked ones,
-      two launches timed as one (start of the first to end of the second).
+      two launches timed as one (start of the first to end of the second);
+      1 read (fence_calib_read, one float written per wave) over the LM
+      head's table bytes, 128256 x 4096 Q8_0, three sets.
     For each: the library's plain float4 stream (fence_calib_stream) at six
     launch shapes, the fastest kept, timed like the ops (kernel start/end
     events); and for the first two torch's own elementwise kernel on the same
@@ -1370,6 +1379,31 @@ def practical_ceiling(torch, F, reps):
               f"({100 * tr['frac_peak']:.1f}%)", file=sys.stderr, flush=True)
         del sets
         torch.cuda.empty_cache()
+
+    # a GEMV's weight stream: one read over the LM head's table bytes
+    # (128256 x 4096 Q8_0), three sets as lm_head_gemv rotates
+    n = (L3_VOCAB * (L3_HIDDEN // 32) * 34) // 16 * 4
+    sets = [torch.randn(n, device="cuda", generator=gen) for _ in range(3)]
+    shapes = {}
+    best = None
+    for t, v in CALIB_SHAPES:
+        waves = -(-n // (4 * t * v)) * t // 64
+        sums = torch.empty(waves, device="cuda")
+        nbytes = 4 * n + 4 * waves
+        r = summary(ours(sets, lambda x, t=t, v=v, s=sums: F.calib_read(s.data_ptr(), x.data_ptr(), n, t, v, sh),
+                         nbytes), nbytes, kernel="calib_read_kernel", threads=t, float4_per_lane=v)
+        shapes[f"{t}x{v}"] = r["GBps"]
+        if best is None or r["us_mean"] < best["us_mean"]:
+            best = r
+        del sums
+    best["GBps_by_shape"] = shapes
+    best["sets"] = len(sets)
+    best["timing"] = "kernel start/end events of each launch (hipExtLaunchKernel)"
+    out["stream_1r"] = best
+    print(f"[ceiling] 1r: stream {best['GBps']:.1f} GB/s ({100 * best['frac_peak']:.1f}%, "
+          f"{best['threads']}x{best['float4_per_lane']})", file=sys.stderr, flush=True)
+    del sets
+    torch.cuda.empty_cache()
 
     # the causal softmax's mix: scores in place, then the masked zeros
     n_rw, n_w = causal_softmax_mix()

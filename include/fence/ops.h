@@ -422,6 +422,16 @@ int fence_time_next_launches(hipEvent_t start, hipEvent_t stop, int count);
 int fence_calib_stream(float* out, const float* a, const float* b, int64_t n, int threads, int vpt,
                        hipStream_t stream);
 
+/* Read-only calibration stream: reads a[0, n) with the same loads and launch
+ * shapes as fence_calib_stream, and wave w writes the sum of the floats it
+ * read to sums[w], where lanes t of workgroup g read the float4s
+ * g * threads * vpt + t + j * threads (j < vpt) and wave w = g * threads / 64
+ * + t / 64: sums holds ceil(n / (4 * threads * vpt)) * threads / 64 floats.
+ * n % 4 == 0, a 16-byte aligned, n / 4 <= 2^30, threads 64 or 256, vpt 1, 2
+ * or 4, else EINVAL.  No counterpart in the reference; the benchmark times it
+ * as the attainable rate of a GEMV's weight stream (one read, no write). */
+int fence_calib_read(float* sums, const float* a, int64_t n, int threads, int vpt, hipStream_t stream);
+
 /* Static text for a status code. */
 const char* fence_status_string(int status);
 

@@ -162,6 +162,13 @@ def _raw(name):
     ("fence_calib_stream", (16, 32, None, 8, 64, 3, None)),        # vpt not 1, 2 or 4
     ("fence_calib_stream", (16, 32, None, 8 << 30, 64, 1, None)),  # past one launch
     ("fence_calib_stream", (16, None, 48, 8, 64, 1, None)),        # b without a
+    ("fence_calib_read", (None, 32, 8, 64, 1, None)),               # no sums
+    ("fence_calib_read", (16, None, 8, 64, 1, None)),               # no input
+    ("fence_calib_read", (16, 32, 6, 64, 1, None)),                 # n % 4 != 0
+    ("fence_calib_read", (16, 0x1008, 8, 64, 1, None)),             # a not 16-byte aligned
+    ("fence_calib_read", (16, 32, 8, 128, 1, None)),                # threads not 64 or 256
+    ("fence_calib_read", (16, 32, 8, 64, 3, None)),                 # vpt not 1, 2 or 4
+    ("fence_calib_read", (16, 32, 8 << 30, 64, 1, None)),           # past one launch
 ])
 def test_invalid_arguments_rejected_on_host(fence, name, args):
     assert _raw(name)(*args) == EINVAL
