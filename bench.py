@@ -473,6 +473,9 @@ def main():
         lm_head["frac_of_ceiling"] = round(lm_head["GBps"] / c, 4)
         lm_head["ceiling_source"] = "practical_ceiling.stream_1r (a plain read-only float4 stream over the " \
                                     "table's bytes, same rotation)"
+    if "stream_1r" in ceiling and isinstance(decode_model, dict) and "GBps_fused" in decode_model:
+        decode_model["frac_of_read_ceiling_fused"] = round(
+            decode_model["GBps_fused"] / ceiling["stream_1r"]["GBps"], 4)
 
     cpu = None if args.no_cpu else section("cpu_baseline", lambda: cpu_baseline(args.cpu_seconds))
     cpu_all = None if args.no_cpu else section("cpu_baseline_all_cores",
