@@ -28,6 +28,8 @@
 
 // Rows whose loads one wave issues together, and the most workgroups (of 4
 // waves) per CU in the grid; the grid never exceeds what is resident at once.
+// FENCE_GEMV_Q8_WG_PER_CU, when defined, sets the staged kernel's cap for
+// every K (otherwise q8_staged_wg_per_cu below).
 #ifndef FENCE_GEMV_Q8_ROWS
 #define FENCE_GEMV_Q8_ROWS 1
 #endif
@@ -36,9 +38,6 @@
 #endif
 #ifndef FENCE_GEMV_Q8_PREFETCH
 #define FENCE_GEMV_Q8_PREFETCH 1
-#endif
-#ifndef FENCE_GEMV_Q8_WG_PER_CU
-#define FENCE_GEMV_Q8_WG_PER_CU 8
 #endif
 
 namespace fence {
@@ -346,39 +345,55 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_empty_kernel(float* __
     if (r < M) y[r] = 0.0f;
 }
 
+// The staged kernel's workgroups per CU for rows of K weights: below the
+// occupancy limit (7 per CU at K = 2560), the best of caps 2-8 measured on
+// the two LM-head shapes, 151936 x 2560 (4: 63-64 us against 66-67 at the
+// limit, 70-72 at 2 or 3) and 128256 x 4096 (3: 86-87 us against 89-90);
+// other K take 4.
+constexpr int q8_staged_wg_per_cu(int K) {
+#ifdef FENCE_GEMV_Q8_WG_PER_CU
+    return static_cast<void>(K), FENCE_GEMV_Q8_WG_PER_CU;
+#else
+    return K == 4096 ? 3 : 4;
+#endif
+}
+
 // Workgroups that fit on the device at once for `kernel` with `lds` bytes of
-// dynamic LDS, capped at FENCE_GEMV_Q8_WG_PER_CU per CU.  Cached per
+// dynamic LDS, at most `cap` per CU.  The occupancy query is cached per
 // (kernel, device): a template instance's static is one per kernel.
 template <class Kernel>
-int resident_grid(Kernel kernel, size_t lds, unsigned* grid) {
+int resident_grid(Kernel kernel, size_t lds, int cap, unsigned* grid) {
     static std::atomic<int> cache[64];
+    static std::atomic<int> cache_cus[64];
     static std::atomic<size_t> cache_lds[64];
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e);
     if (dev < 0 || dev >= 64) return FENCE_ERROR_INVALID_VALUE;
-    int g = cache[dev].load(std::memory_order_acquire);
-    if (g == 0 || cache_lds[dev].load(std::memory_order_relaxed) != lds) {
-        int cus = 0, per_cu = 0;
+    int per_cu = cache[dev].load(std::memory_order_acquire);
+    int cus = cache_cus[dev].load(std::memory_order_relaxed);
+    if (per_cu == 0 || cus == 0 || cache_lds[dev].load(std::memory_order_relaxed) != lds) {
         if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev); e != hipSuccess)
             return hip_status(e);
         if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGemvThreads, lds);
             e != hipSuccess)
             return hip_status(e);
-        if (per_cu > FENCE_GEMV_Q8_WG_PER_CU) per_cu = FENCE_GEMV_Q8_WG_PER_CU;
         if (per_cu < 1) per_cu = 1;
-        g = cus * per_cu;
+        if (cus < 1) cus = 1;
         cache_lds[dev].store(lds, std::memory_order_relaxed);
-        cache[dev].store(g, std::memory_order_release);
+        cache_cus[dev].store(cus, std::memory_order_relaxed);
+        cache[dev].store(per_cu, std::memory_order_release);
     }
-    *grid = static_cast<unsigned>(g);
+    // a grid read against another lds's entry is still a valid grid (every
+    // kernel strides over its rows); only its size would be off
+    *grid = static_cast<unsigned>(cus * (per_cu < cap ? per_cu : cap));
     return FENCE_SUCCESS;
 }
 
 template <class Kernel>
 int launch_rows(Kernel kernel, float* y, const uint8_t* W, const float* x, int M, int K, int rows_per_wave,
-                size_t lds, hipStream_t s) {
+                size_t lds, hipStream_t s, int cap = 8) {
     unsigned grid = 0;
-    if (int st = resident_grid(kernel, lds, &grid); st != FENCE_SUCCESS) return st;
+    if (int st = resident_grid(kernel, lds, cap, &grid); st != FENCE_SUCCESS) return st;
     const int64_t per_wg = static_cast<int64_t>(kGemvThreads / kWave) * rows_per_wave;
     const int64_t wanted = (M + per_wg - 1) / per_wg;
     if (wanted < grid) grid = static_cast<unsigned>(wanted);
@@ -391,8 +406,9 @@ int launch_slots(float* y, const uint8_t* W, const float* x, int M, int K, hipSt
     if (FENCE_GEMV_Q8_STAGED && K % 256 == 0 && aligned(W, 16)) {
         const size_t lds = static_cast<size_t>(kGemvThreads / kWave) * (K / 32) * 34 + 16;
         constexpr int pf = FENCE_GEMV_Q8_PREFETCH;
-        if (full) return launch_rows(gemv_q8_0_staged_kernel<SLOTS, true, pf>, y, W, x, M, K, 1, lds, s);
-        return launch_rows(gemv_q8_0_staged_kernel<SLOTS, false, pf>, y, W, x, M, K, 1, lds, s);
+        const int cap = q8_staged_wg_per_cu(K);
+        if (full) return launch_rows(gemv_q8_0_staged_kernel<SLOTS, true, pf>, y, W, x, M, K, 1, lds, s, cap);
+        return launch_rows(gemv_q8_0_staged_kernel<SLOTS, false, pf>, y, W, x, M, K, 1, lds, s, cap);
     }
     if (full)
         return launch_rows(gemv_q8_0_kernel<SLOTS, FENCE_GEMV_Q8_ROWS, true>, y, W, x, M, K, FENCE_GEMV_Q8_ROWS, 0, s);
