@@ -345,16 +345,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_empty_kernel(float* __
     if (r < M) y[r] = 0.0f;
 }
 
-// The staged kernel's workgroups per CU for rows of K weights: below the
-// occupancy limit (7 per CU at K = 2560), the best of caps 2-8 measured on
-// the two LM-head shapes, 151936 x 2560 (4: 63-64 us against 66-67 at the
-// limit, 70-72 at 2 or 3) and 128256 x 4096 (3: 86-87 us against 89-90);
-// other K take 4.
+// The staged kernel's workgroups per CU: 4, below the occupancy limit (7 per
+// CU at K = 2560).  Of caps 2-8 on the two LM-head shapes, 4 is the best at
+// 151936 x 2560 (63-64 us against 66-67 at the limit, 70-72 at 2 or 3) and
+// level with the limit at 128256 x 4096 (89-92 us); 3 there ran 86-87 us in
+// a process of its own but 93-96 after the rest of a benchmark run.
 constexpr int q8_staged_wg_per_cu(int K) {
 #ifdef FENCE_GEMV_Q8_WG_PER_CU
     return static_cast<void>(K), FENCE_GEMV_Q8_WG_PER_CU;
 #else
-    return K == 4096 ? 3 : 4;
+    return static_cast<void>(K), 4;
 #endif
 }
 
