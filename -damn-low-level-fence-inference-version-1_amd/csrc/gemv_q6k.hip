@@ -55,6 +55,13 @@
 // interleaved runs each): 1,852 and 1,854 us per token with 1 against 1,768
 // and 1,767 with 0 -- wave lifetimes vary by several us within a launch
 // whatever the group count, so fewer workgroups only lose parallelism.
+// Most workgroups per CU in a resident grid (0: as many as fit).  6 trims
+// the 4-wave launches (down: 7 fit, o: 8) and leaves the 8-wave ones (2
+// fit); decode steps ran ~10 us per token faster than with every resident
+// workgroup, and slower with 5 (+15-20 us) or level with 4.
+#ifndef FENCE_GEMV_Q6K_WG_PER_CU
+#define FENCE_GEMV_Q6K_WG_PER_CU 6
+#endif
 #ifndef FENCE_GEMV_Q6K_BALANCED
 #define FENCE_GEMV_Q6K_BALANCED 0
 #endif
@@ -1097,6 +1104,7 @@ int launch_grid_as(OccKernel occ_kernel, Kernel kernel, int threads, std::atomic
         if (hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, occ_kernel, threads, 0);
             e != hipSuccess)
             return hip_status(e);
+        if (FENCE_GEMV_Q6K_WG_PER_CU > 0 && per_cu > FENCE_GEMV_Q6K_WG_PER_CU) per_cu = FENCE_GEMV_Q6K_WG_PER_CU;
         g = cus * (per_cu > 0 ? per_cu : 1);
         cache[dev].store(g, std::memory_order_relaxed);
     }
